@@ -1,0 +1,264 @@
+"""Benchmark of the paged-KV attention path on one MI355X.
+
+Headline (the JSON line's value): bf16 paged decode at the Qwen3-8B shape
+(32 q / 8 kv heads, head_dim 128, block_size 256, 4096-block pool, 64
+sequences with context U[2048, 8192], seed 1).  A step is one pass of the
+path over the batch: the store of every sequence's new token, then the
+decode.  value = algorithmic decode bytes (every visible K/V element once,
+q read, o written) / step time, in GB/s.
+
+Also reported on the same line: prefill TFLOP/s at the Qwen3-8B shape (16
+sequences, new U[512, 4096] over 0-8 cached blocks, seed 2), quantised
+decode tokens/s (256 sequences, ctx U[1024, 4096], fp8 / int8 / bf16, seed
+3), the mixed chunked-prefill + decode step at a Qwen3-32B-like shape (seed
+4), the dominant kernel's roofline fraction (HIP events on the launch
+stream) and the CPU eager restatement timed on the host cores.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only decode|prefill|quant|mixed]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+import torch
+
+HBM_PEAK_GBS = 8000.0      # MI355X HBM3E, AMD published
+BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, AMD published
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def timed_steps(fn, steps: int, warmup: int):
+    """W untimed calls, then K timed calls bracketed by synchronize; returns
+    (ms per step, per-call event ms list measured on the current stream)."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for a, b in ev:
+        a.record(stream)
+        fn()
+        b.record(stream)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    return wall, [a.elapsed_time(b) for a, b in ev]
+
+
+def attention_only(wl):
+    a = wl.attn
+    fn = a.prefill_flashattn if a.forward_backend in ("flashattn", "hip") else a.prefill_torch
+    return lambda: fn(wl.q, wl.k, wl.v, wl.context)
+
+
+def step(wl):
+    return lambda: wl.attn.forward(wl.q, wl.k, wl.v, wl.context)
+
+
+def bench_decode(steps, warmup):
+    from nanovllm_self_amd import workloads as W
+
+    log("building decode_8b (bf16)")
+    wl = W.decode_8b("cuda")
+    nbytes = wl.decode_bytes()
+    ms_step, _ = timed_steps(step(wl), steps, warmup)
+    _, ev = timed_steps(attention_only(wl), steps, warmup)
+    ms_attn = statistics.median(ev)
+    res = {
+        "bytes": nbytes,
+        "ms_per_step": ms_step,
+        "gbs_step": nbytes / ms_step / 1e6,
+        "ms_attention": ms_attn,
+        "gbs_attention": nbytes / ms_attn / 1e6,
+        "tokens_per_s": wl.num_seqs / (ms_step / 1e3),
+    }
+    log(f"decode_8b: {ms_step:.3f} ms/step, attention {ms_attn:.3f} ms -> {res['gbs_attention']:.0f} GB/s")
+    return wl, res
+
+
+def bench_prefill(steps, warmup):
+    from nanovllm_self_amd import workloads as W
+
+    log("building prefill_8b")
+    wl = W.prefill_8b("cuda")
+    flops = wl.prefill_flops()
+    ms_step, _ = timed_steps(step(wl), steps, warmup)
+    _, ev = timed_steps(attention_only(wl), steps, warmup)
+    ms_attn = statistics.median(ev)
+    res = {
+        "workload": "prefill_8b: 32q/8kv heads, D128, bs256, 16 seqs, new U[512,4096] over 0-8 cached blocks, seed 2",
+        "flops": flops,
+        "ms_per_step": ms_step,
+        "ms_attention": ms_attn,
+        "tflops": flops / ms_attn / 1e9,
+        "frac_bf16_peak": flops / ms_attn / 1e9 / BF16_PEAK_TFLOPS,
+        "tokens_per_s": sum(s.num_new_tokens for s in wl.seqs) / (ms_step / 1e3),
+    }
+    log(f"prefill_8b: attention {ms_attn:.3f} ms -> {res['tflops']:.0f} TFLOP/s")
+    del wl
+    return res
+
+
+def bench_quant(steps, warmup):
+    from nanovllm_self_amd import workloads as W
+
+    out = {"workload": "decode_quant: 32q/8kv heads, D128, bs256, 256 seqs, ctx U[1024,4096], 1% outliers x8, seed 3"}
+    for kv in ("bf16", "fp8", "int8"):
+        log(f"building decode_quant ({kv})")
+        wl = W.decode_quant("cuda", kv=kv)
+        nbytes = wl.decode_bytes()
+        ms_step, _ = timed_steps(step(wl), steps, warmup)
+        _, ev = timed_steps(attention_only(wl), steps, warmup)
+        ms_attn = statistics.median(ev)
+        out[kv] = {
+            "bytes": nbytes,
+            "ms_per_step": ms_step,
+            "ms_attention": ms_attn,
+            "gbs_attention": nbytes / ms_attn / 1e6,
+            "tokens_per_s": wl.num_seqs / (ms_step / 1e3),
+        }
+        log(f"decode_quant/{kv}: {ms_step:.3f} ms/step -> {out[kv]['tokens_per_s']:.0f} tok/s")
+        del wl
+        torch.cuda.empty_cache()
+    out["fp8_vs_bf16_tokens"] = out["fp8"]["tokens_per_s"] / out["bf16"]["tokens_per_s"]
+    out["int8_vs_bf16_tokens"] = out["int8"]["tokens_per_s"] / out["bf16"]["tokens_per_s"]
+    return out
+
+
+def bench_mixed(steps, warmup):
+    from nanovllm_self_amd import workloads as W
+
+    out = {"workload": "mixed_32b: 64q/8kv heads, 128 decode seqs ctx logU[256,32768] + 4 x 2048-token chunks over U[0,16384] cached, 16384 blocks, seed 4"}
+    for kv in ("bf16", "fp8"):
+        log(f"building mixed_32b ({kv})")
+        wl = W.mixed_32b("cuda", kv=kv)
+        ms_step, _ = timed_steps(step(wl), steps, warmup)
+        dec_b, pf = wl.decode_bytes(), wl.prefill_flops()
+        t_roof = dec_b / (HBM_PEAK_GBS * 1e9) + pf / (BF16_PEAK_TFLOPS * 1e12)
+        out[kv] = {
+            "ms_per_step": ms_step,
+            "decode_bytes": dec_b,
+            "prefill_flops": pf,
+            "roofline_ms": t_roof * 1e3,
+            "frac_roofline": t_roof * 1e3 / ms_step,
+        }
+        log(f"mixed_32b/{kv}: {ms_step:.3f} ms/step (roofline {t_roof * 1e3:.3f} ms)")
+        del wl
+        torch.cuda.empty_cache()
+    return out
+
+
+def cpu_baseline(wl, decode_res):
+    """The eager restatement (gather + per-sequence fp32 attention) on the
+    host cores, over a bounded sample of the decode batch."""
+    import numpy as np
+
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from tests.gpu_util import oracle_paged
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    ids = list(range(4))
+    lens = [wl.seqs[i].num_cached_tokens + 1 for i in ids]
+    H, D = wl.num_kv_heads, wl.head_dim
+    nbytes = sum(lens) * H * 2 * D * 2 + len(ids) * wl.num_heads * D * 4
+    oracle_paged(wl, ids)  # warm-up
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        oracle_paged(wl, ids)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    return {
+        "value": nbytes / t / 1e9,
+        "unit": "GB/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"decode_8b sequences 0-3 ({sum(lens)} context tokens): gather + fp32 attention, median of 3",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--only", choices=["decode", "prefill", "quant", "mixed"], default=None)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (the path has no multi-GPU code); got --gpus {args.gpus}",
+              file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(2)
+    from nanovllm_self_amd import _lib
+
+    _lib.load()
+    torch.cuda.set_device(0)
+    steps, warmup = args.steps, args.warmup
+
+    if args.only == "prefill":
+        print(json.dumps(bench_prefill(steps, warmup)))
+        return
+    if args.only == "quant":
+        print(json.dumps(bench_quant(steps, warmup)))
+        return
+    if args.only == "mixed":
+        print(json.dumps(bench_mixed(steps, warmup)))
+        return
+
+    wl, dec = bench_decode(steps, warmup)
+    line = {
+        "metric": "paged-decode attn GB/s (%HBM peak) + prefill attn TFLOP/s, Qwen3-8B shape",
+        "value": round(dec["gbs_step"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(dec["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "decode_8b: Qwen3-8B attention layer, 32q/8kv heads, D128, bf16 KV, block 256, "
+                        "4096-block pool, 64 seqs ctx U[2048,8192] (seed 1); step = store + decode",
+            "global_batch": wl.num_seqs,
+            "seq_len": wl.context.max_seqlen_k,
+            "parallelism": "none (1 GPU)",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "paged_attention decode call (split-K decode + partition merge)",
+            "achieved": round(dec["gbs_attention"], 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(dec["gbs_attention"] / HBM_PEAK_GBS, 4),
+            "traffic": None,
+        },
+        "decode_8b": dec,
+    }
+    if args.only is None:
+        if not args.no_cpu:
+            log("cpu baseline")
+            line["cpu_baseline"] = cpu_baseline(wl, dec)
+        del wl
+        torch.cuda.empty_cache()
+        line["prefill_8b"] = bench_prefill(max(5, steps // 4), 2)
+        line["decode_quant"] = bench_quant(steps, warmup)
+        line["mixed_32b"] = bench_mixed(max(5, steps // 4), 2)
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

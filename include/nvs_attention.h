@@ -1,0 +1,210 @@
+/*
+ * nvs_attention.h — C ABI of the MI355X (gfx950) paged-KV attention library
+ * (libnvs_attention.so).
+ *
+ * These entry points replace the tensor-level operations behind
+ * nanovllm/layers/attention.py:PagedAttention in the reference (nanovllm_self):
+ * the KV-cache write, the per-token KV quantisation, the paged gather used by
+ * the eager path, and the varlen / paged causal attention that the reference
+ * delegates to flash_attn_varlen_func.  Each declaration cites the reference
+ * code it replaces.
+ *
+ * Conventions shared by every entry point
+ *  - All pointers are device pointers owned by the caller; the library never
+ *    allocates, frees or retains them.  `stream` is a hipStream_t (NULL = the
+ *    default stream).  Every call is asynchronous on `stream`: no host sync,
+ *    no device allocation, so calls are safe inside HIP-graph capture as long
+ *    as the caller's buffers stay alive.
+ *  - Strides are in elements, not bytes.  The innermost (head_dim) dimension
+ *    of every tensor must be contiguous.
+ *  - KV cache layout (reference model_runner.py:40-50, 302-331): one layer's
+ *    K (or V) cache is a contiguous [num_blocks, block_size, num_kv_heads,
+ *    head_dim] array; a token at slot s = block_id * block_size + offset lives
+ *    at element offset (s * num_kv_heads + h) * head_dim.  Quantised caches add
+ *    a contiguous fp32 scale array [num_blocks, block_size, num_kv_heads]
+ *    (reference model_runner.py:52-73, the trailing dim of 1 is implicit).
+ *  - Return value: NVS_OK (0) on success, a negative NVS_ERR_* code otherwise;
+ *    nvs_last_error() then returns a message describing the failure (per
+ *    calling thread).  Arguments are validated before anything is launched.
+ */
+#ifndef NVS_ATTENTION_H
+#define NVS_ATTENTION_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types.  INT8 is the reference's "int8_mock" symmetric per-token,
+ * per-kv-head quantisation (attention.py:63-98); FP8_E4M3 is OCP
+ * float8_e4m3fn with the same per-token, per-kv-head scale layout. */
+enum nvs_dtype {
+  NVS_DTYPE_BF16 = 0,
+  NVS_DTYPE_FP16 = 1,
+  NVS_DTYPE_FP32 = 2,
+  NVS_DTYPE_INT8 = 3,
+  NVS_DTYPE_FP8_E4M3 = 4
+};
+
+enum nvs_status {
+  NVS_OK = 0,
+  NVS_ERR_INVALID = -1,     /* bad shape / stride / pointer argument   */
+  NVS_ERR_UNSUPPORTED = -2, /* valid request this build does not serve */
+  NVS_ERR_WORKSPACE = -3,   /* workspace missing or too small          */
+  NVS_ERR_LAUNCH = -4       /* HIP reported an error at launch         */
+};
+
+/* Message for the last failing call on this thread ("" if none). */
+const char* nvs_last_error(void);
+
+/* Library version, major * 10000 + minor * 100 + patch. */
+int nvs_version(void);
+
+/*
+ * KV-cache write.  Replaces PagedAttention.store_kv_cache_torch
+ * (reference attention.py:139-189, dispatched from write_kv_cache :120-136).
+ *   k, v          [num_tokens, num_kv_heads, head_dim] of src_dtype
+ *                 (BF16 / FP16 / FP32), strides (tok, head) in elements.
+ *   slot_mapping  [num_tokens] int32; block = slot / block_size, offset =
+ *                 slot % block_size.  Slots < 0 are skipped (padding rows);
+ *                 slots >= num_blocks * block_size are skipped as well, so
+ *                 the kernel never writes outside the cache.
+ *   cache_dtype   BF16 / FP16 / FP32: the row is cast to the cache dtype with
+ *                 round-to-nearest-even (the reference's k.to(cache_dtype)).
+ *                 INT8: absmax = max|x| over head_dim in fp32,
+ *                 scale = max(absmax / 127, 1e-6),
+ *                 code = clamp(rint(x / scale), -127, 127), bit-exact with
+ *                 quantize_int8_per_token (attention.py:94-98).
+ *                 FP8_E4M3: scale = max(absmax / 448, 1e-6),
+ *                 code = e4m3fn(clamp(x / scale, -448, 448)) with RNE.
+ *   k_scale, v_scale  fp32 scale caches, required for INT8 / FP8_E4M3,
+ *                 ignored otherwise.
+ *   head_dim must be a multiple of 8 with head_dim / 8 a power of two <= 64.
+ */
+int nvs_store_kvcache(const void* k, const void* v, int src_dtype,
+                      int64_t k_tok_stride, int64_t k_head_stride,
+                      int64_t v_tok_stride, int64_t v_head_stride,
+                      const int32_t* slot_mapping, int64_t num_tokens,
+                      void* k_cache, void* v_cache, int cache_dtype,
+                      float* k_scale, float* v_scale,
+                      int64_t num_blocks, int block_size, int num_kv_heads,
+                      int head_dim, void* stream);
+
+/*
+ * Per-token, per-head quantisation of a [num_tokens, num_heads, head_dim]
+ * tensor into contiguous codes (same shape) and fp32 scales
+ * [num_tokens, num_heads].  Replaces PagedAttention.quantize_int8_per_token
+ * (reference attention.py:63-98); code_dtype INT8 or FP8_E4M3, same
+ * arithmetic as nvs_store_kvcache.
+ */
+int nvs_quantize_per_token(const void* x, int src_dtype, int64_t tok_stride,
+                           int64_t head_stride, int64_t num_tokens,
+                           int num_heads, int head_dim, void* codes,
+                           int code_dtype, float* scales, void* stream);
+
+/*
+ * Dequantisation (codes * scale) rounded to out_dtype (BF16 / FP16 / FP32),
+ * contiguous [num_tokens, num_heads, head_dim] in and out, scales
+ * [num_tokens, num_heads].  Replaces dequantize_int8_per_token
+ * (reference attention.py:100-117).
+ */
+int nvs_dequantize_per_token(const void* codes, int code_dtype,
+                             const float* scales, int64_t num_tokens,
+                             int num_heads, int head_dim, void* out,
+                             int out_dtype, void* stream);
+
+/*
+ * Paged gather of the visible K/V of a batch, the eager path's
+ * PagedAttention.get_kv_cache (reference attention.py:201-285).
+ * For sequence i the non-negative entries of block_tables[i] are taken in
+ * order (entries < 0 are dropped, as row[row != -1] does), flattened to
+ * tokens and truncated to context_lens[i]; codes are dequantised to out_dtype
+ * when cache_dtype is INT8 / FP8_E4M3, otherwise cast.  Positions past the
+ * gathered length are zero and kv_mask (uint8, [num_seqs, max_len]) is 1
+ * exactly on gathered positions.
+ *   k_out, v_out  contiguous [num_seqs, max_len, num_kv_heads, head_dim].
+ */
+int nvs_gather_kvcache(const void* k_cache, const void* v_cache,
+                       int cache_dtype, const float* k_scale,
+                       const float* v_scale, const int32_t* block_tables,
+                       int64_t bt_stride, int max_blocks_per_seq,
+                       const int32_t* context_lens, int num_seqs, int max_len,
+                       int64_t num_blocks, int block_size, int num_kv_heads,
+                       int head_dim, void* k_out, void* v_out, int out_dtype,
+                       uint8_t* kv_mask, void* stream);
+
+/*
+ * Workspace (bytes) that nvs_paged_attention needs for the split-K decode
+ * partials of a batch with these bounds.  0 is a valid answer.
+ */
+int64_t nvs_attention_workspace_bytes(int num_seqs, int max_seqlen_q,
+                                      int max_seqlen_k, int num_heads,
+                                      int num_kv_heads, int head_dim,
+                                      int block_size);
+
+/*
+ * Causal varlen attention over a paged KV cache: the paged call of
+ * prefill_flashattn (reference attention.py:356-375,
+ * flash_attn_varlen_func(..., block_table=...)) and equally the
+ * prefix branch of prefill_torch (attention.py:441-498).  Serves prefix-hit
+ * prefill, chunked prefill, decode (q_len == 1) and mixed batches in one call.
+ *   q             [num_tokens, num_heads, head_dim] BF16, strides in elements.
+ *   cu_seqlens_q  [num_seqs + 1] int32 prefix sums of the new-token counts.
+ *   cu_seqlens_k  [num_seqs + 1] int32 prefix sums of the visible KV lengths
+ *                 (cached prefix + new tokens, already written to the cache).
+ *   block_tables  [num_seqs, bt_stride] int32; logical block j of sequence i
+ *                 is block_tables[i * bt_stride + j]; entries < 0 read as
+ *                 all-zero K and V (the eager path's zero padding).
+ *   Mask: query row r of a sequence with q_len new and k_len visible tokens
+ *   attends keys j <= r + (k_len - q_len) (bottom-right causal); rows with no
+ *   visible key produce 0.  GQA: query head hq reads kv head
+ *   hq / (num_heads / num_kv_heads).
+ *   cache_dtype   BF16, INT8 or FP8_E4M3 (scales required for the last two).
+ *   out           [num_tokens, num_heads, head_dim] BF16.
+ *   Rows with q_len == 1 run the split-K decode kernels and need `workspace`
+ *   of at least nvs_attention_workspace_bytes(...) bytes.
+ *   head_dim must be 128; num_heads / num_kv_heads must be 1..16;
+ *   block_size must be a multiple of 64.
+ */
+int nvs_paged_attention(const void* q, int64_t q_tok_stride,
+                        int64_t q_head_stride, const void* k_cache,
+                        const void* v_cache, int cache_dtype,
+                        const float* k_scale, const float* v_scale,
+                        const int32_t* cu_seqlens_q,
+                        const int32_t* cu_seqlens_k,
+                        const int32_t* block_tables, int64_t bt_stride,
+                        int num_seqs, int64_t num_tokens, int max_seqlen_q,
+                        int max_seqlen_k, int num_heads, int num_kv_heads,
+                        int head_dim, int block_size, int64_t num_blocks,
+                        float softmax_scale, void* out, int64_t out_tok_stride,
+                        int64_t out_head_stride, void* workspace,
+                        int64_t workspace_bytes, void* stream);
+
+/*
+ * Causal varlen attention over the step's own (not cached) K/V: the
+ * block_tables-is-None call of prefill_flashattn (reference
+ * attention.py:338-354, flash_attn_varlen_func without block_table) and the
+ * no-prefix branch of prefill_torch (attention.py:400-439).
+ *   k, v          [num_tokens, num_kv_heads, head_dim] BF16 with strides;
+ *                 keys of sequence i are rows cu_seqlens_k[i] ..
+ *                 cu_seqlens_k[i+1]-1.  Same mask, GQA map and output as
+ *                 nvs_paged_attention; head_dim 128.
+ */
+int nvs_varlen_attention(const void* q, int64_t q_tok_stride,
+                         int64_t q_head_stride, const void* k, const void* v,
+                         int64_t k_tok_stride, int64_t k_head_stride,
+                         int64_t v_tok_stride, int64_t v_head_stride,
+                         const int32_t* cu_seqlens_q,
+                         const int32_t* cu_seqlens_k, int num_seqs,
+                         int64_t num_tokens, int max_seqlen_q,
+                         int max_seqlen_k, int num_heads, int num_kv_heads,
+                         int head_dim, float softmax_scale, void* out,
+                         int64_t out_tok_stride, int64_t out_head_stride,
+                         void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NVS_ATTENTION_H */

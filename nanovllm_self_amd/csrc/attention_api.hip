@@ -1,0 +1,114 @@
+// C ABI of the attention kernels: argument validation and dispatch of decode
+// rows (q_len == 1, split-K decode) and prefill rows (MFMA flash prefill).
+#include "nvs_common.h"
+#include "attention_common.h"
+
+using namespace nvs;
+
+static int validate_common(const AttnParams& P, const char* who) {
+  NVS_REQUIRE(P.B >= 0 && P.T >= 0, NVS_ERR_INVALID, "%s: negative batch size", who);
+  NVS_REQUIRE(P.B < 65536, NVS_ERR_UNSUPPORTED, "%s: at most 65535 sequences per call", who);
+  NVS_REQUIRE(P.q && P.out && P.cu_q && P.cu_k, NVS_ERR_INVALID, "%s: null tensor pointer", who);
+  NVS_REQUIRE(P.Hq > 0 && P.Hkv > 0 && P.Hq % P.Hkv == 0, NVS_ERR_INVALID,
+              "%s: num_heads (%d) must be a positive multiple of num_kv_heads (%d)", who, P.Hq,
+              P.Hkv);
+  NVS_REQUIRE(P.Hq / P.Hkv <= 16, NVS_ERR_UNSUPPORTED,
+              "%s: at most 16 query heads per kv head, got %d", who, P.Hq / P.Hkv);
+  NVS_REQUIRE(P.max_seqlen_q >= 0 && P.max_seqlen_k >= 0, NVS_ERR_INVALID,
+              "%s: negative max_seqlen", who);
+  NVS_REQUIRE(P.q_ts % 8 == 0 && P.q_hs % 8 == 0 && ((uintptr_t)P.q % 16) == 0, NVS_ERR_INVALID,
+              "%s: q rows must be 16-byte aligned", who);
+  NVS_REQUIRE(P.out_ts % 8 == 0 && P.out_hs % 8 == 0 && ((uintptr_t)P.out % 16) == 0,
+              NVS_ERR_INVALID, "%s: out rows must be 16-byte aligned", who);
+  return NVS_OK;
+}
+
+extern "C" int64_t nvs_attention_workspace_bytes(int num_seqs, int max_seqlen_q, int max_seqlen_k,
+                                                 int num_heads, int num_kv_heads, int head_dim,
+                                                 int block_size) {
+  (void)max_seqlen_q;
+  (void)num_kv_heads;
+  (void)head_dim;
+  (void)block_size;
+  if (num_seqs <= 0 || num_heads <= 0) return 0;
+  return decode_workspace_bytes(num_seqs, max_seqlen_k, num_heads);
+}
+
+extern "C" int nvs_paged_attention(const void* q, int64_t q_tok_stride, int64_t q_head_stride,
+                                   const void* k_cache, const void* v_cache, int cache_dtype,
+                                   const float* k_scale, const float* v_scale,
+                                   const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                                   const int32_t* block_tables, int64_t bt_stride, int num_seqs,
+                                   int64_t num_tokens, int max_seqlen_q, int max_seqlen_k,
+                                   int num_heads, int num_kv_heads, int head_dim, int block_size,
+                                   int64_t num_blocks, float softmax_scale, void* out,
+                                   int64_t out_tok_stride, int64_t out_head_stride,
+                                   void* workspace, int64_t workspace_bytes, void* stream) {
+  clear_error();
+  AttnParams P = {};
+  P.q = q; P.q_ts = q_tok_stride; P.q_hs = q_head_stride;
+  P.kc = k_cache; P.vc = v_cache; P.cache_dtype = cache_dtype; P.ks = k_scale; P.vs = v_scale;
+  P.bt = block_tables; P.bt_stride = bt_stride; P.bs = block_size; P.NB = num_blocks;
+  P.cu_q = cu_seqlens_q; P.cu_k = cu_seqlens_k;
+  P.B = num_seqs; P.T = num_tokens; P.max_seqlen_q = max_seqlen_q; P.max_seqlen_k = max_seqlen_k;
+  P.Hq = num_heads; P.Hkv = num_kv_heads; P.softmax_scale = softmax_scale;
+  P.out = out; P.out_ts = out_tok_stride; P.out_hs = out_head_stride;
+  P.ws = workspace; P.ws_bytes = workspace_bytes;
+  if (num_seqs == 0 || num_tokens == 0) return NVS_OK;
+  int rc = validate_common(P, "paged_attention");
+  if (rc != NVS_OK) return rc;
+  NVS_REQUIRE(head_dim == kHeadDim, NVS_ERR_UNSUPPORTED,
+              "paged_attention: head_dim must be %d, got %d", kHeadDim, head_dim);
+  NVS_REQUIRE(k_cache && v_cache && block_tables, NVS_ERR_INVALID,
+              "paged_attention: null cache / block_tables pointer");
+  NVS_REQUIRE(cache_dtype == NVS_DTYPE_BF16 || cache_dtype == NVS_DTYPE_INT8 ||
+                  cache_dtype == NVS_DTYPE_FP8_E4M3,
+              NVS_ERR_UNSUPPORTED, "paged_attention: cache dtype %d not served (bf16/int8/fp8)",
+              cache_dtype);
+  NVS_REQUIRE(!is_quant(cache_dtype) || (k_scale && v_scale), NVS_ERR_INVALID,
+              "paged_attention: quantised cache needs k_scale and v_scale");
+  NVS_REQUIRE(block_size > 0 && block_size % 64 == 0, NVS_ERR_UNSUPPORTED,
+              "paged_attention: block_size must be a multiple of 64, got %d", block_size);
+  NVS_REQUIRE(num_blocks > 0, NVS_ERR_INVALID, "paged_attention: empty cache");
+  NVS_REQUIRE(bt_stride > 0 && ((int64_t)max_seqlen_k + block_size - 1) / block_size <= bt_stride,
+              NVS_ERR_INVALID,
+              "paged_attention: block_tables rows (%lld) too short for max_seqlen_k %d",
+              (long long)bt_stride, max_seqlen_k);
+  if (max_seqlen_q <= 0) return NVS_OK;
+  hipStream_t s = (hipStream_t)stream;
+  rc = launch_decode(P, s);
+  if (rc != NVS_OK || max_seqlen_q == 1) return rc;
+  return launch_prefill(P, /*skip_decode_rows=*/true, s);
+}
+
+extern "C" int nvs_varlen_attention(const void* q, int64_t q_tok_stride, int64_t q_head_stride,
+                                    const void* k, const void* v, int64_t k_tok_stride,
+                                    int64_t k_head_stride, int64_t v_tok_stride,
+                                    int64_t v_head_stride, const int32_t* cu_seqlens_q,
+                                    const int32_t* cu_seqlens_k, int num_seqs, int64_t num_tokens,
+                                    int max_seqlen_q, int max_seqlen_k, int num_heads,
+                                    int num_kv_heads, int head_dim, float softmax_scale, void* out,
+                                    int64_t out_tok_stride, int64_t out_head_stride,
+                                    void* stream) {
+  clear_error();
+  AttnParams P = {};
+  P.q = q; P.q_ts = q_tok_stride; P.q_hs = q_head_stride;
+  P.k = k; P.v = v; P.k_ts = k_tok_stride; P.k_hs = k_head_stride;
+  P.v_ts = v_tok_stride; P.v_hs = v_head_stride;
+  P.bt = nullptr;
+  P.cu_q = cu_seqlens_q; P.cu_k = cu_seqlens_k;
+  P.B = num_seqs; P.T = num_tokens; P.max_seqlen_q = max_seqlen_q; P.max_seqlen_k = max_seqlen_k;
+  P.Hq = num_heads; P.Hkv = num_kv_heads; P.softmax_scale = softmax_scale;
+  P.out = out; P.out_ts = out_tok_stride; P.out_hs = out_head_stride;
+  if (num_seqs == 0 || num_tokens == 0) return NVS_OK;
+  int rc = validate_common(P, "varlen_attention");
+  if (rc != NVS_OK) return rc;
+  NVS_REQUIRE(head_dim == kHeadDim, NVS_ERR_UNSUPPORTED,
+              "varlen_attention: head_dim must be %d, got %d", kHeadDim, head_dim);
+  NVS_REQUIRE(k && v, NVS_ERR_INVALID, "varlen_attention: null k/v pointer");
+  NVS_REQUIRE(k_tok_stride % 8 == 0 && k_head_stride % 8 == 0 && v_tok_stride % 8 == 0 &&
+                  v_head_stride % 8 == 0 && ((uintptr_t)k % 16) == 0 && ((uintptr_t)v % 16) == 0,
+              NVS_ERR_INVALID, "varlen_attention: k/v rows must be 16-byte aligned");
+  if (max_seqlen_q <= 0) return NVS_OK;
+  return launch_prefill(P, /*skip_decode_rows=*/false, (hipStream_t)stream);
+}

@@ -1,0 +1,182 @@
+"""KV pool, layer binding and step-metadata builders for the paged attention.
+
+These are the producer side of the attention boundary in the reference:
+
+- KVCacheConfig mirrors the hot-path knobs of nanovllm/config.py:28-80
+  (kv_cache_dtype, attention_compute_dtype, kv_cache_quant_mode,
+  kv_cache_scale_dtype, block_size) including the rule that a quantised mode
+  forces the cache dtype (config.py:78-80).  Quant modes: "none", "int8_mock"
+  (reference) and "fp8_e4m3" (OCP float8_e4m3fn codes, same per-token,
+  per-kv-head fp32 scale layout).
+- allocate_kv_cache mirrors model_runner.py:40-73: kv_cache
+  [2, L, NB, bs, Hkv, D] and, for quantised modes, kv_scale_cache
+  [2, L, NB, bs, Hkv, 1].
+- bind_kv_cache mirrors bind_kvcache_to_attention (model_runner.py:302-331).
+  The reference pins int8 to forward_backend="torch" (:323-324) because
+  flash-attn cannot read int8; the HIP kernels serve int8 and fp8 on every
+  backend, so the backend is left as the caller set it.
+- prepare_block_tables mirrors model_runner.py:334-344 (rows padded with -1).
+- build_context mirrors prepare_model_input (model_runner.py:461-532) with the
+  per-token slot loop vectorised.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Iterable, Sequence
+
+import numpy as np
+import torch
+
+from .utils.context import Context, get_context
+
+KV_QUANT_MODES = ("none", "int8_mock", "fp8_e4m3")
+
+_DTYPE_ALIASES = {
+    "float32": torch.float32,
+    "fp32": torch.float32,
+    "float16": torch.float16,
+    "fp16": torch.float16,
+    "bfloat16": torch.bfloat16,
+    "bf16": torch.bfloat16,
+}
+
+
+def resolve_torch_dtype(dtype):
+    """String alias or torch dtype -> torch dtype; None / "auto" -> None (config.py:6-25)."""
+    if isinstance(dtype, torch.dtype):
+        return dtype
+    if dtype in (None, "auto"):
+        return None
+    if dtype not in _DTYPE_ALIASES:
+        raise ValueError(f"unsupported dtype: {dtype}")
+    return _DTYPE_ALIASES[dtype]
+
+
+@dataclass
+class KVCacheConfig:
+    dtype: torch.dtype | str = torch.bfloat16
+    kv_cache_dtype: torch.dtype | str = torch.bfloat16
+    attention_compute_dtype: torch.dtype | str = torch.bfloat16
+    kv_cache_quant_mode: str = "none"
+    kv_cache_scale_dtype: torch.dtype | str = "fp32"
+    block_size: int = 256
+    num_blocks: int = 256
+
+    def __post_init__(self):
+        self.dtype = resolve_torch_dtype(self.dtype) or torch.float16
+        self.kv_cache_dtype = resolve_torch_dtype(self.kv_cache_dtype) or self.dtype
+        self.attention_compute_dtype = resolve_torch_dtype(self.attention_compute_dtype) or self.dtype
+        self.kv_cache_scale_dtype = resolve_torch_dtype(self.kv_cache_scale_dtype) or torch.float32
+        if self.kv_cache_quant_mode not in KV_QUANT_MODES:
+            raise ValueError(f"unsupported kv_cache_quant_mode: {self.kv_cache_quant_mode}")
+        if self.kv_cache_quant_mode == "int8_mock":
+            self.kv_cache_dtype = torch.int8
+        elif self.kv_cache_quant_mode == "fp8_e4m3":
+            self.kv_cache_dtype = torch.float8_e4m3fn
+        if self.kv_cache_quant_mode != "none" and self.kv_cache_scale_dtype != torch.float32:
+            raise ValueError("quantised KV caches keep fp32 scales")
+
+
+def allocate_kv_cache(
+    num_layers: int,
+    num_kv_heads: int,
+    head_dim: int,
+    cfg: KVCacheConfig,
+    device: torch.device | str,
+):
+    """Zeroed kv_cache [2, L, NB, bs, Hkv, D] and, when quantised, a
+    kv_scale_cache [2, L, NB, bs, Hkv, 1] of ones (model_runner.py:40-73)."""
+    kv_cache = torch.zeros(
+        2, num_layers, cfg.num_blocks, cfg.block_size, num_kv_heads, head_dim,
+        dtype=cfg.kv_cache_dtype, device=device,
+    )
+    kv_scale_cache = None
+    if cfg.kv_cache_quant_mode != "none":
+        kv_scale_cache = torch.ones(
+            2, num_layers, cfg.num_blocks, cfg.block_size, num_kv_heads, 1,
+            dtype=cfg.kv_cache_scale_dtype, device=device,
+        )
+    return kv_cache, kv_scale_cache
+
+
+def bind_kv_cache(attn_layers: Iterable, kv_cache, kv_scale_cache, cfg: KVCacheConfig) -> None:
+    """Bind per-layer K/V (and scale) views onto PagedAttention modules."""
+    for layer_id, p_attn in enumerate(attn_layers):
+        p_attn.k_cache = kv_cache[0, layer_id]
+        p_attn.v_cache = kv_cache[1, layer_id]
+        p_attn.block_size = cfg.block_size
+        p_attn.layer_id = layer_id
+        p_attn.kv_cache_quant_mode = cfg.kv_cache_quant_mode
+        p_attn.kv_cache_dtype = cfg.kv_cache_dtype
+        p_attn.attention_compute_dtype = cfg.attention_compute_dtype
+        if kv_scale_cache is not None:
+            p_attn.k_scale_cache = kv_scale_cache[0, layer_id]
+            p_attn.v_scale_cache = kv_scale_cache[1, layer_id]
+        else:
+            p_attn.k_scale_cache = None
+            p_attn.v_scale_cache = None
+
+
+def prepare_block_tables(block_tables: Sequence[Sequence[int]], device) -> torch.Tensor:
+    """Pad per-sequence block lists with -1 into an int32 [B, max_blocks] tensor."""
+    max_len = max(len(bt) for bt in block_tables)
+    rows = [list(bt) + [-1] * (max_len - len(bt)) for bt in block_tables]
+    t = torch.tensor(rows, dtype=torch.int32)
+    if torch.device(device).type == "cuda":
+        t = t.pin_memory().to(device, non_blocking=True)
+    return t
+
+
+@dataclass
+class SeqSlice:
+    """What the step needs of one sequence (the Sequence fields the runner reads)."""
+
+    block_table: Sequence[int]
+    num_cached_tokens: int
+    num_new_tokens: int
+    need_logits: bool = True
+
+
+def build_context(seqs: Sequence[SeqSlice], block_size: int, device) -> Context:
+    """Step metadata exactly as prepare_model_input forms it.
+
+    Query tokens of a sequence are positions [num_cached, num_cached + num_new);
+    its visible KV length is num_cached + num_new; the slot of position p is
+    block_table[p // block_size] * block_size + p % block_size; block_tables
+    is only built when some sequence sees more keys than it brings queries.
+    """
+    cu_q = [0]
+    cu_k = [0]
+    ctx_lens, need = [], []
+    slots = []
+    for i, s in enumerate(seqs):
+        start = s.num_cached_tokens
+        end = start + s.num_new_tokens
+        cu_q.append(cu_q[-1] + s.num_new_tokens)
+        cu_k.append(cu_k[-1] + end)
+        ctx_lens.append(end)
+        if s.need_logits:
+            need.append(i)
+        pos = np.arange(start, end, dtype=np.int64)
+        bt = np.asarray(s.block_table, dtype=np.int64)
+        slots.append(bt[pos // block_size] * block_size + pos % block_size)
+    slot_mapping = np.concatenate(slots) if slots else np.zeros(0, dtype=np.int64)
+    max_q = max((s.num_new_tokens for s in seqs), default=0)
+    max_k = max(ctx_lens, default=0)
+    block_tables = None
+    if cu_k[-1] > cu_q[-1]:
+        block_tables = prepare_block_tables([s.block_table for s in seqs], device)
+
+    def i32(x):
+        return torch.as_tensor(np.asarray(x, dtype=np.int32)).to(device)
+
+    return get_context(
+        cu_seqlens_q=i32(cu_q),
+        cu_seqlens_k=i32(cu_k),
+        max_seqlen_q=max_q,
+        max_seqlen_k=max_k,
+        slot_mapping=i32(slot_mapping),
+        context_lens=i32(ctx_lens),
+        block_tables=block_tables,
+        seq_need_compute_logits=i32(need),
+    )

@@ -1,0 +1,397 @@
+"""Drop-in PagedAttention backed by hand-written gfx950 HIP kernels.
+
+Mirrors nanovllm/layers/attention.py:PagedAttention of the reference
+(nanovllm_self): same constructor, attributes the model runner binds
+(model_runner.py:302-331), method names the engine and tests call, forward
+semantics and error messages.  The tensor work is done by libnvs_attention.so
+(include/nvs_attention.h); there is no eager fallback, so every path fails
+loudly when the library or a GPU is missing.
+
+Backends: forward_backend "flashattn" (reference default) and "hip" run
+prefill_flashattn; "torch" runs prefill_torch.  Both reach the same HIP
+kernels; they differ only in the guards prefill_flashattn applies
+(attention.py:319-336).  Quantised caches ("int8_mock", "fp8_e4m3") are served
+by both.
+"""
+from __future__ import annotations
+
+import math
+from time import perf_counter
+
+import torch
+import torch.nn as nn
+
+from .. import _lib
+from ..utils.context import Context
+
+_COMPUTE_DTYPES = (torch.bfloat16,)
+_SERVED_CACHE_DTYPES = (torch.bfloat16, torch.int8, torch.float8_e4m3fn)
+_QUANT_DTYPE = {"int8_mock": torch.int8, "fp8_e4m3": torch.float8_e4m3fn}
+
+_workspaces: dict = {}
+
+
+def _need_device(t: torch.Tensor, what: str) -> None:
+    if not t.is_cuda:
+        raise RuntimeError(f"{what} must be a GPU tensor for the HIP kernels (got {t.device})")
+
+
+def attention_workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
+    """Per-device split-K workspace, grown on demand (never inside graph capture)."""
+    if nbytes <= 0:
+        return None
+    key = torch.device(device)
+    buf = _workspaces.get(key)
+    if buf is None or buf.numel() < nbytes:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError(
+                "decode workspace too small inside graph capture; call "
+                "reserve_attention_workspace(...) before capturing"
+            )
+        buf = torch.empty(nbytes, dtype=torch.uint8, device=key)
+        _workspaces[key] = buf
+    return buf
+
+
+def reserve_attention_workspace(num_seqs: int, max_seqlen_k: int, num_heads: int, device) -> None:
+    """Pre-size the workspace for batches up to these bounds."""
+    n = _lib.load().nvs_attention_workspace_bytes(num_seqs, 1, max_seqlen_k, num_heads, 0, 128, 0)
+    attention_workspace(torch.device(device), int(n))
+
+
+def _quantize(x: torch.Tensor, code_dtype: torch.dtype):
+    """[N, H, D] -> (codes [N, H, D], fp32 scales [N, H, 1])."""
+    _need_device(x, "x")
+    if x.dim() != 3 or x.stride(-1) != 1:
+        raise RuntimeError("quantize expects [num_tokens, num_heads, head_dim] with contiguous head_dim")
+    n, h, d = x.shape
+    codes = torch.empty((n, h, d), dtype=code_dtype, device=x.device)
+    scales = torch.empty((n, h, 1), dtype=torch.float32, device=x.device)
+    lib = _lib.load()
+    _lib.check(
+        lib.nvs_quantize_per_token(
+            x.data_ptr(), _lib.nvs_dtype(x.dtype), x.stride(0), x.stride(1), n, h, d,
+            codes.data_ptr(), _lib.nvs_dtype(code_dtype), scales.data_ptr(), _lib.stream_of(x),
+        ),
+        "quantize_per_token",
+    )
+    return codes, scales
+
+
+def _dequantize(q: torch.Tensor, scale: torch.Tensor, out_dtype: torch.dtype) -> torch.Tensor:
+    _need_device(q, "q")
+    q = q.contiguous()
+    scale = scale.to(torch.float32).contiguous()
+    d = q.shape[-1]
+    h = q.shape[-2] if q.dim() >= 2 else 1
+    n = q.numel() // (h * d)
+    if scale.numel() != n * h:
+        raise RuntimeError("scale must hold one value per (token, head)")
+    out = torch.empty(q.shape, dtype=out_dtype, device=q.device)
+    lib = _lib.load()
+    _lib.check(
+        lib.nvs_dequantize_per_token(
+            q.data_ptr(), _lib.nvs_dtype(q.dtype), scale.data_ptr(), n, h, d,
+            out.data_ptr(), _lib.nvs_dtype(out_dtype), _lib.stream_of(q),
+        ),
+        "dequantize_per_token",
+    )
+    return out
+
+
+class PagedAttention(nn.Module):
+    """Paged-KV attention layer; call it per decoder layer with the step's
+    q [T, Hq, D], k, v [T, Hkv, D] and the step Context."""
+
+    def __init__(self, num_heads, num_kv_heads, head_dim, dtype=torch.bfloat16):
+        super().__init__()
+        self.num_heads = num_heads
+        self.head_dim = head_dim
+        self.num_kv_heads = num_kv_heads
+        self.groups = num_heads // num_kv_heads if num_kv_heads > 0 else 1
+        self.dtype = dtype
+
+        self.kv_cache_dtype = torch.float16
+        self.attention_compute_dtype = torch.float16
+        self.decode_backend = "paged_flash"
+        self.prefill_backend = "hip"
+
+        self.kv_cache_quant_mode = "none"
+        self.k_scale_cache = None
+        self.v_scale_cache = None
+
+        # Bound per layer by the model runner.
+        self.k_cache = None
+        self.v_cache = None
+        self.block_size = None
+        self.layer_id = None
+
+        self.enable_profile = False
+        self.profile_decode = dict(
+            store=0.0, load=0.0, attn=0.0, gqa_expand=0.0, permute=0.0,
+            qk=0.0, softmax=0.0, av=0.0, calls=0,
+        )
+        # No synchronisation or host timing while a graph is being captured.
+        self.in_cuda_graph_capture = False
+
+        self.kv_writer_backend = "torch"
+        self.forward_backend = "flashattn"
+
+    def _should_profile(self):
+        return self.enable_profile and (not self.in_cuda_graph_capture)
+
+    # ------------------------------------------------------------------ quant
+    def quantize_int8_per_token(self, x):
+        """Symmetric per-token, per-head int8: scale = max(absmax/127, 1e-6),
+        q = clamp(round_half_even(x / scale), -127, 127) (attention.py:63-98)."""
+        return _quantize(x, torch.int8)
+
+    def quantize_fp8_per_token(self, x):
+        """Per-token, per-head OCP e4m3: scale = max(absmax/448, 1e-6),
+        q = e4m3(clamp(x / scale, -448, 448)) with round-to-nearest-even."""
+        return _quantize(x, torch.float8_e4m3fn)
+
+    def dequantize_int8_per_token(self, q, scale):
+        """(q.float() * scale) rounded to attention_compute_dtype
+        (attention.py:100-117); int8 or e4m3 codes."""
+        return _dequantize(q, scale, self.attention_compute_dtype)
+
+    # ------------------------------------------------------------------ store
+    def write_kv_cache(self, k, v, slot_mapping):
+        """KV write entry point (attention.py:120-136)."""
+        if self.kv_writer_backend in ("torch", "hip"):
+            return self.store_kv_cache_torch(k, v, slot_mapping)
+        raise NotImplementedError(f"unknown kv writer backend: {self.kv_writer_backend}")
+
+    def store_kv_cache_torch(self, k, v, slot_mapping):
+        """Write k, v [T, Hkv, D] to the cache slots (attention.py:139-189).
+
+        Name kept for drop-in compatibility; runs nvs_store_kvcache.  Plain
+        caches receive k.to(cache dtype); quantised modes write codes and
+        per-token, per-kv-head fp32 scales.  Negative slots are skipped.
+        """
+        kc, vc = self.k_cache, self.v_cache
+        if kc is None or vc is None:
+            raise RuntimeError("k_cache / v_cache are not bound")
+        for t, name in ((k, "k"), (v, "v"), (kc, "k_cache"), (vc, "v_cache"), (slot_mapping, "slot_mapping")):
+            _need_device(t, name)
+        mode = self.kv_cache_quant_mode
+        if mode in _QUANT_DTYPE:
+            if kc.dtype != _QUANT_DTYPE[mode]:
+                raise RuntimeError(f"{mode} KV cache must be {_QUANT_DTYPE[mode]}, got {kc.dtype}")
+            if self.k_scale_cache is None or self.v_scale_cache is None:
+                raise RuntimeError(f"{mode} KV cache needs k_scale_cache / v_scale_cache")
+        elif mode != "none":
+            raise ValueError(f"unsupported kv_cache_quant_mode: {mode}")
+        elif kc.dtype in (torch.int8, torch.float8_e4m3fn):
+            raise RuntimeError(f"cache dtype {kc.dtype} needs a quantised kv_cache_quant_mode")
+        if k.stride(-1) != 1 or v.stride(-1) != 1:
+            raise RuntimeError("k / v need a contiguous head_dim")
+        if not kc.is_contiguous() or not vc.is_contiguous():
+            raise RuntimeError("k_cache / v_cache must be contiguous [num_blocks, block_size, Hkv, D]")
+        if slot_mapping.dtype != torch.int32:
+            slot_mapping = slot_mapping.to(torch.int32)
+        slot_mapping = slot_mapping.contiguous()
+        if v.dtype != k.dtype:
+            v = v.to(k.dtype)
+        num_blocks, block_size, hkv, d = kc.shape
+        ks = self.k_scale_cache if mode in _QUANT_DTYPE else None
+        vs = self.v_scale_cache if mode in _QUANT_DTYPE else None
+        if ks is not None and (ks.dtype != torch.float32 or not ks.is_contiguous() or not vs.is_contiguous()):
+            raise RuntimeError("scale caches must be contiguous fp32 [num_blocks, block_size, Hkv, 1]")
+        lib = _lib.load()
+        _lib.check(
+            lib.nvs_store_kvcache(
+                k.data_ptr(), v.data_ptr(), _lib.nvs_dtype(k.dtype),
+                k.stride(0), k.stride(1), v.stride(0), v.stride(1),
+                slot_mapping.data_ptr(), k.shape[0],
+                kc.data_ptr(), vc.data_ptr(), _lib.nvs_dtype(kc.dtype),
+                _lib.ptr(ks), _lib.ptr(vs),
+                num_blocks, block_size, hkv, d, _lib.stream_of(k),
+            ),
+            "store_kvcache",
+        )
+
+    # ----------------------------------------------------------------- gather
+    def get_kv_cache(self, context):
+        """Visible K/V of the batch gathered to [B, max_len, Hkv, D] plus the
+        validity mask (attention.py:201-285), via nvs_gather_kvcache."""
+        bt = context.block_tables.to(torch.int32).contiguous()
+        seq_lens = context.context_lens.to(torch.int32).contiguous()
+        batch_size = bt.size(0)
+        max_len = int(seq_lens.max().item())
+        mode = self.kv_cache_quant_mode
+        out_dtype = self.attention_compute_dtype if mode in _QUANT_DTYPE else self.k_cache.dtype
+        if mode not in _QUANT_DTYPE and self.attention_compute_dtype is not None:
+            out_dtype = self.attention_compute_dtype
+        dev = self.k_cache.device
+        k_batch = torch.empty(batch_size, max_len, self.num_kv_heads, self.head_dim, dtype=out_dtype, device=dev)
+        v_batch = torch.empty_like(k_batch)
+        kv_mask = torch.empty(batch_size, max_len, dtype=torch.bool, device=dev)
+        kc = self.k_cache
+        num_blocks, block_size = kc.shape[0], kc.shape[1]
+        ks = self.k_scale_cache if mode in _QUANT_DTYPE else None
+        vs = self.v_scale_cache if mode in _QUANT_DTYPE else None
+        lib = _lib.load()
+        _lib.check(
+            lib.nvs_gather_kvcache(
+                kc.data_ptr(), self.v_cache.data_ptr(), _lib.nvs_dtype(kc.dtype),
+                _lib.ptr(ks), _lib.ptr(vs), bt.data_ptr(), bt.stride(0), bt.size(1),
+                seq_lens.data_ptr(), batch_size, max_len, num_blocks, block_size,
+                self.num_kv_heads, self.head_dim, k_batch.data_ptr(), v_batch.data_ptr(),
+                _lib.nvs_dtype(out_dtype), kv_mask.data_ptr(), _lib.stream_of(kc),
+            ),
+            "gather_kvcache",
+        )
+        return k_batch, v_batch, kv_mask
+
+    # -------------------------------------------------------------- attention
+    def _attention(self, q, k, v, context):
+        """One call of the HIP attention over the whole (mixed) batch."""
+        compute = torch.bfloat16
+        if q.dtype != compute:
+            q = q.to(compute)
+        _need_device(q, "q")
+        if q.stride(-1) != 1:
+            q = q.contiguous()
+        T = q.shape[0]
+        out = torch.empty(T, self.num_heads, self.head_dim, dtype=compute, device=q.device)
+        cu_q = context.cu_seqlens_q.to(torch.int32).contiguous()
+        cu_k = context.cu_seqlens_k.to(torch.int32).contiguous()
+        B = cu_q.numel() - 1
+        scale = 1.0 / math.sqrt(self.head_dim)
+        lib = _lib.load()
+        stream = _lib.stream_of(q)
+        if context.block_tables is None:
+            k = k.to(compute) if k.dtype != compute else k
+            v = v.to(compute) if v.dtype != compute else v
+            if k.stride(-1) != 1:
+                k = k.contiguous()
+            if v.stride(-1) != 1:
+                v = v.contiguous()
+            _lib.check(
+                lib.nvs_varlen_attention(
+                    q.data_ptr(), q.stride(0), q.stride(1),
+                    k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1), v.stride(0), v.stride(1),
+                    cu_q.data_ptr(), cu_k.data_ptr(), B, T,
+                    int(context.max_seqlen_q), int(context.max_seqlen_k),
+                    self.num_heads, self.num_kv_heads, self.head_dim, scale,
+                    out.data_ptr(), out.stride(0), out.stride(1), stream,
+                ),
+                "varlen_attention",
+            )
+        else:
+            kc, vc = self.k_cache, self.v_cache
+            if kc.dtype not in _SERVED_CACHE_DTYPES:
+                raise RuntimeError(f"HIP attention serves bf16/int8/fp8 KV caches, got {kc.dtype}")
+            mode = self.kv_cache_quant_mode
+            quant = kc.dtype in (torch.int8, torch.float8_e4m3fn)
+            if quant and mode not in _QUANT_DTYPE:
+                raise RuntimeError(f"cache dtype {kc.dtype} needs a quantised kv_cache_quant_mode")
+            ks = self.k_scale_cache if quant else None
+            vs = self.v_scale_cache if quant else None
+            if quant and (ks is None or vs is None):
+                raise RuntimeError("quantised KV cache needs k_scale_cache / v_scale_cache")
+            bt = context.block_tables
+            if bt.dtype != torch.int32 or not bt.is_contiguous():
+                bt = bt.to(torch.int32).contiguous()
+            num_blocks, block_size = kc.shape[0], kc.shape[1]
+            max_q, max_k = int(context.max_seqlen_q), int(context.max_seqlen_k)
+            ws_bytes = int(lib.nvs_attention_workspace_bytes(
+                B, max_q, max_k, self.num_heads, self.num_kv_heads, self.head_dim, block_size))
+            ws = attention_workspace(q.device, ws_bytes)
+            _lib.check(
+                lib.nvs_paged_attention(
+                    q.data_ptr(), q.stride(0), q.stride(1),
+                    kc.data_ptr(), vc.data_ptr(), _lib.nvs_dtype(kc.dtype), _lib.ptr(ks), _lib.ptr(vs),
+                    cu_q.data_ptr(), cu_k.data_ptr(), bt.data_ptr(), bt.size(1),
+                    B, T, max_q, max_k, self.num_heads, self.num_kv_heads, self.head_dim,
+                    block_size, num_blocks, scale, out.data_ptr(), out.stride(0), out.stride(1),
+                    _lib.ptr(ws), ws_bytes, stream,
+                ),
+                "paged_attention",
+            )
+        return out if self.dtype == compute else out.to(self.dtype)
+
+    def prefill(self, q, k, v, context):
+        """Write KV, then attend with the selected backend (attention.py:288-301)."""
+        self.write_kv_cache(k, v, context.slot_mapping)
+        if self.forward_backend == "torch":
+            return self.prefill_torch(q, k, v, context)
+        elif self.forward_backend in ("flashattn", "hip"):
+            return self.prefill_flashattn(q, k, v, context)
+        raise NotImplementedError(f"unknown prefill backend: {self.forward_backend}")
+
+    def prefill_flashattn(self, q, k, v, context):
+        """Unified varlen attention (attention.py:303-375): plain varlen over
+        the step's k/v when block_tables is None, otherwise paged over the
+        cache (prefix prefill, chunked prefill, decode, mixed batches)."""
+        if self.k_cache.dtype not in (torch.float16, torch.bfloat16, torch.int8, torch.float8_e4m3fn):
+            raise RuntimeError(
+                f"flashattn only supports fp16/bf16 kv cache (or int8/fp8 codes), got {self.k_cache.dtype}"
+            )
+        if self.kv_cache_quant_mode == "none" and self.k_cache.dtype != self.attention_compute_dtype:
+            raise RuntimeError(
+                f"flashattn only supports the same dtype, got {self.k_cache.dtype} and "
+                f"{self.attention_compute_dtype}"
+            )
+        return self._attention(q, k, v, context)
+
+    def prefill_torch(self, q, k, v, context):
+        """Unified-semantics attention of the eager path (attention.py:378-498):
+        no prefix -> causal over the step's k/v; with block_tables -> the
+        cached (dequantised) K/V with the bottom-right causal mask."""
+        return self._attention(q, k, v, context)
+
+    def forward_unified(self, q, k, v, context):
+        """Write the step's K/V, then one attention call over the whole batch
+        (attention.py:500-546)."""
+        should_profile = self._should_profile()
+        if should_profile:
+            torch.cuda.synchronize()
+            t0 = perf_counter()
+
+        self.write_kv_cache(k, v, context.slot_mapping)
+
+        if should_profile:
+            torch.cuda.synchronize()
+            self.profile_decode["store"] += perf_counter() - t0
+
+        if self.forward_backend == "torch":
+            fn = self.prefill_torch
+        elif self.forward_backend in ("flashattn", "hip"):
+            fn = self.prefill_flashattn
+        else:
+            raise NotImplementedError(f"unknown decode backend: {self.decode_backend}")
+        if should_profile:
+            torch.cuda.synchronize()
+            t0 = perf_counter()
+        out = fn(q, k, v, context)
+        if should_profile:
+            torch.cuda.synchronize()
+            self.profile_decode["attn"] += perf_counter() - t0
+            self.profile_decode["calls"] += 1
+        return out
+
+    def forward(self, q, k, v, context):
+        return self.forward_unified(q, k, v, context)
+
+    def decode_flashattn(self, q, context):
+        """Decode-only entry (attention.py:552-584): q [B, Hq, D] against the
+        cache through context.block_tables / context_lens."""
+        B = q.shape[0]
+        dev = q.device
+        lens = context.context_lens.to(torch.int32)
+        cu_q = torch.arange(B + 1, dtype=torch.int32, device=dev)
+        cu_k = torch.zeros(B + 1, dtype=torch.int32, device=dev)
+        cu_k[1:] = torch.cumsum(lens, 0)
+        ctx = Context(
+            cu_seqlens_q=cu_q, cu_seqlens_k=cu_k, max_seqlen_q=1,
+            max_seqlen_k=int(context.max_seqlen_k) or int(lens.max().item()),
+            context_lens=lens, block_tables=context.block_tables,
+        )
+        return self._attention(q, None, None, ctx)
+
+
+# The name the attention layer goes by in the engine's documentation.
+Attention = PagedAttention

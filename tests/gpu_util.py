@@ -1,0 +1,87 @@
+"""Helpers shared by the GPU parity tests (not a test module)."""
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import torch
+
+from oracle import attn_oracle as AO
+from oracle import kv_oracle as KO
+
+BF16_MAX_ABS, BF16_MEAN_ABS = 2e-2, 2e-3  # bf16 KV vs the fp32 oracle
+QUANT_MAX_ABS = 5e-2                       # int8 / fp8 KV vs the fp32 oracle
+
+
+def say(*args):
+    """Name the case before a GPU step (flushed, so it survives a crash)."""
+    print("[case]", *args, file=sys.stderr, flush=True)
+
+
+def bf16_to_np(t: torch.Tensor) -> np.ndarray:
+    return KO.bf16_bits_to_f32(t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16))
+
+
+def cache_blocks_f32(attn, blocks: np.ndarray):
+    """Dequantised float32 copies of the given cache blocks, as the eager
+    path sees them: bf16 caches as stored; int8 / fp8 codes * scale rounded
+    to bf16 (dequantize_int8_per_token's .to(attention_compute_dtype))."""
+    idx = torch.as_tensor(blocks, dtype=torch.long, device=attn.k_cache.device)
+    out = []
+    for cache, scale in ((attn.k_cache, attn.k_scale_cache), (attn.v_cache, attn.v_scale_cache)):
+        sub = cache.index_select(0, idx).cpu()
+        if sub.dtype == torch.bfloat16:
+            out.append(bf16_to_np(sub))
+            continue
+        codes = sub.view(torch.uint8).numpy()
+        kind = "int8" if sub.dtype == torch.int8 else "fp8"
+        if kind == "int8":
+            codes = codes.view(np.int8)
+        sc = scale.index_select(0, idx).cpu().numpy()
+        out.append(KO.round_to_bf16(KO.dequantize_per_token(codes, sc, kind)))
+    return out[0], out[1]
+
+
+def oracle_paged(wl, seq_ids):
+    """fp32 oracle output rows of the given sequences of a paged workload.
+    Only their blocks are copied from the device; block ids are remapped onto
+    that compact pool."""
+    ctx = wl.context
+    cu_q = ctx.cu_seqlens_q.cpu().tolist()
+    bs = wl.block_size
+    blocks, tables, lens, qrows, qlens = [], [], [], [], []
+    for i in seq_ids:
+        s = wl.seqs[i]
+        n = s.num_cached_tokens + s.num_new_tokens
+        need = (n + bs - 1) // bs
+        tb = list(s.block_table[:need])
+        tables.append(list(range(len(blocks), len(blocks) + len(tb))))
+        blocks.extend(tb)
+        lens.append(n)
+        qrows.extend(range(cu_q[i], cu_q[i + 1]))
+        qlens.append(s.num_new_tokens)
+    kv, vv = cache_blocks_f32(wl.attn, np.asarray(blocks))
+    width = max(len(t) for t in tables)
+    bt = np.full((len(seq_ids), width), -1, dtype=np.int64)
+    for r, t in enumerate(tables):
+        bt[r, : len(t)] = t
+    q = torch.from_numpy(bf16_to_np(wl.q[torch.as_tensor(qrows, device=wl.q.device)]))
+    sub_cu_q = np.concatenate([[0], np.cumsum(qlens)]).tolist()
+    sub_cu_k = np.concatenate([[0], np.cumsum(lens)]).tolist()
+    out = AO.paged_attention(q, kv, vv, bt, sub_cu_q, sub_cu_k, lens, wl.num_heads, wl.num_kv_heads,
+                             wl.head_dim)
+    return out.numpy(), qrows
+
+
+def compare(got: np.ndarray, ref: np.ndarray, quant: bool, what: str):
+    assert got.shape == ref.shape, (got.shape, ref.shape)
+    assert np.all(np.isfinite(got)), f"{what}: non-finite output"
+    err = np.abs(got.astype(np.float64) - ref.astype(np.float64))
+    mx, mean = float(err.max()), float(err.mean())
+    say(f"{what}: max-abs {mx:.3e} mean-abs {mean:.3e}")
+    if quant:
+        assert mx <= QUANT_MAX_ABS, f"{what}: max-abs {mx:.3e} > {QUANT_MAX_ABS}"
+    else:
+        assert mx <= BF16_MAX_ABS, f"{what}: max-abs {mx:.3e} > {BF16_MAX_ABS}"
+        assert mean <= BF16_MEAN_ABS, f"{what}: mean-abs {mean:.3e} > {BF16_MEAN_ABS}"
+    return mx, mean

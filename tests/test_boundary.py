@@ -1,0 +1,179 @@
+"""The drop-in boundary, on the CPU: library exports, Context fields, the
+KV-pool/config knobs, the step-metadata builder and the guards that fire
+before any launch."""
+import dataclasses
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from nanovllm_self_amd import PagedAttention, Attention, _lib
+from nanovllm_self_amd.kv_cache import (
+    KVCacheConfig, SeqSlice, allocate_kv_cache, bind_kv_cache, build_context, prepare_block_tables,
+)
+from nanovllm_self_amd.utils.context import Context, get_context
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def test_library_exports_every_declared_symbol():
+    header = (ROOT / "include" / "nvs_attention.h").read_text()
+    declared = set(re.findall(r"\b(nvs_[a-z0-9_]+)\s*\(", header))
+    assert declared, "no declarations parsed"
+    lib = _lib.load()
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert declared == set(_lib.SIGNATURES), declared ^ set(_lib.SIGNATURES)
+    assert lib.nvs_version() >= 100
+
+
+def test_context_fields_match_reference():
+    # nanovllm/utils/context.py:5-36
+    names = [f.name for f in dataclasses.fields(Context)]
+    assert names == ["cu_seqlens_q", "cu_seqlens_k", "max_seqlen_q", "max_seqlen_k", "slot_mapping",
+                     "context_lens", "block_tables", "seq_need_compute_logits"]
+    c = get_context(max_seqlen_q=3)
+    assert c.max_seqlen_q == 3 and c.block_tables is None
+
+
+def test_attention_module_surface():
+    a = Attention(32, 8, 128)
+    assert isinstance(a, PagedAttention)
+    assert a.groups == 4 and a.dtype == torch.bfloat16
+    for attr in ("k_cache", "v_cache", "block_size", "layer_id", "kv_cache_quant_mode", "kv_cache_dtype",
+                 "attention_compute_dtype", "forward_backend", "k_scale_cache", "v_scale_cache",
+                 "prefill_backend", "decode_backend", "enable_profile", "profile_decode",
+                 "in_cuda_graph_capture", "kv_writer_backend"):
+        assert hasattr(a, attr), attr
+    assert set(a.profile_decode) == {"store", "load", "attn", "gqa_expand", "permute", "qk", "softmax", "av", "calls"}
+    for m in ("forward", "forward_unified", "write_kv_cache", "store_kv_cache_torch", "get_kv_cache",
+              "prefill_torch", "prefill_flashattn", "quantize_int8_per_token", "dequantize_int8_per_token",
+              "decode_flashattn"):
+        assert callable(getattr(a, m)), m
+
+
+@pytest.mark.parametrize("alias,dt", [("bf16", torch.bfloat16), ("bfloat16", torch.bfloat16),
+                                      ("fp16", torch.float16), ("float16", torch.float16),
+                                      ("fp32", torch.float32), ("float32", torch.float32)])
+def test_config_aliases(alias, dt):
+    # pd_self/evaluation/test_kv_cache_dtype_matrix.py:35-51
+    c = KVCacheConfig(kv_cache_dtype=alias, attention_compute_dtype=alias)
+    assert c.kv_cache_dtype == dt and c.attention_compute_dtype == dt
+
+
+def test_config_quant_modes():
+    assert KVCacheConfig().block_size == 256
+    assert KVCacheConfig().kv_cache_dtype == torch.bfloat16
+    assert KVCacheConfig(kv_cache_quant_mode="int8_mock").kv_cache_dtype == torch.int8
+    assert KVCacheConfig(kv_cache_quant_mode="fp8_e4m3").kv_cache_dtype == torch.float8_e4m3fn
+    with pytest.raises(ValueError, match="unsupported kv_cache_quant_mode"):
+        KVCacheConfig(kv_cache_quant_mode="int4")
+
+
+def test_allocate_and_bind_layout():
+    cfg = KVCacheConfig(kv_cache_quant_mode="fp8_e4m3", block_size=256, num_blocks=3)
+    kv, sc = allocate_kv_cache(2, 4, 128, cfg, "cpu")
+    assert kv.shape == (2, 2, 3, 256, 4, 128) and kv.dtype == torch.float8_e4m3fn
+    assert sc.shape == (2, 2, 3, 256, 4, 1) and sc.dtype == torch.float32 and torch.all(sc == 1)
+    layers = [PagedAttention(8, 4, 128), PagedAttention(8, 4, 128)]
+    bind_kv_cache(layers, kv, sc, cfg)
+    assert layers[1].k_cache.data_ptr() == kv[0, 1].data_ptr() and layers[1].k_cache.is_contiguous()
+    assert layers[0].v_scale_cache.data_ptr() == sc[1, 0].data_ptr()
+    assert layers[1].layer_id == 1 and layers[0].kv_cache_quant_mode == "fp8_e4m3"
+
+
+def test_build_context_matches_reference_formula():
+    # model_runner.py:461-532 on a decode row, a chunk over a prefix and a fresh prompt
+    bs = 4
+    seqs = [SeqSlice([7, 2], 5, 1), SeqSlice([1, 3, 0], 4, 5), SeqSlice([6], 0, 3)]
+    c = build_context(seqs, bs, "cpu")
+    assert c.cu_seqlens_q.tolist() == [0, 1, 6, 9]
+    assert c.cu_seqlens_k.tolist() == [0, 6, 15, 18]
+    assert c.context_lens.tolist() == [6, 9, 3]
+    assert (c.max_seqlen_q, c.max_seqlen_k) == (5, 9)
+    ref = []
+    for s in seqs:
+        for p in range(s.num_cached_tokens, s.num_cached_tokens + s.num_new_tokens):
+            ref.append(s.block_table[p // bs] * bs + p % bs)
+    assert c.slot_mapping.tolist() == ref
+    assert c.block_tables.tolist() == [[7, 2, -1], [1, 3, 0], [6, -1, -1]]
+    assert c.slot_mapping.dtype == torch.int32 and c.block_tables.dtype == torch.int32
+    fresh = build_context([SeqSlice([0], 0, 3), SeqSlice([1], 0, 2)], bs, "cpu")
+    assert fresh.block_tables is None
+    assert prepare_block_tables([[1], [2, 3]], "cpu").tolist() == [[1, -1], [2, 3]]
+
+
+def test_flashattn_guard_rejects_fp32_cache():
+    # pd_self/evaluation/test_kv_cache_dtype_matrix.py:124-140
+    a = PagedAttention(num_heads=8, num_kv_heads=8, head_dim=16)
+    a.k_cache = torch.zeros(1, 256, 8, 16, dtype=torch.float32)
+    a.v_cache = torch.zeros_like(a.k_cache)
+    a.attention_compute_dtype = torch.float32
+    z = torch.zeros(1, 8, 16)
+    with pytest.raises(RuntimeError, match="fp16/bf16 kv cache"):
+        a.prefill_flashattn(z, z, z, context=None)
+
+
+def test_dtype_mismatch_guard():
+    a = PagedAttention(8, 8, 128)
+    a.k_cache = torch.zeros(1, 256, 8, 128, dtype=torch.bfloat16)
+    a.v_cache = torch.zeros_like(a.k_cache)
+    a.attention_compute_dtype = torch.float16
+    z = torch.zeros(1, 8, 128)
+    with pytest.raises(RuntimeError, match="same dtype"):
+        a.prefill_flashattn(z, z, z, context=None)
+
+
+def test_no_cpu_fallback():
+    a = PagedAttention(8, 8, 128)
+    a.block_size = 256
+    a.k_cache = torch.zeros(1, 256, 8, 128, dtype=torch.bfloat16)
+    a.v_cache = torch.zeros_like(a.k_cache)
+    k = torch.zeros(1, 8, 128, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="GPU tensor"):
+        a.store_kv_cache_torch(k, k, torch.zeros(1, dtype=torch.int32))
+    a.kv_writer_backend = "triton"
+    with pytest.raises(NotImplementedError):
+        a.write_kv_cache(k, k, torch.zeros(1, dtype=torch.int32))
+    a.forward_backend = "nope"
+    a.kv_writer_backend = "torch"
+    with pytest.raises((NotImplementedError, RuntimeError)):
+        a.forward(k, k, k, Context(slot_mapping=torch.zeros(1, dtype=torch.int32)))
+
+
+def test_c_abi_validates_before_launch():
+    """Invalid requests are rejected on the host with a message; fake
+    non-null pointers are never dereferenced."""
+    lib = _lib.load()
+    P = 1 << 20  # 16-byte aligned, never touched
+    rc = lib.nvs_paged_attention(P, 1024, 128, P, P, 0, None, None, P, P, P, 8, 1, 1, 1, 256,
+                                 4, 1, 64, 256, 8, 0.125, P, 512, 128, None, 0, None)
+    assert rc == -2 and b"head_dim" in lib.nvs_last_error()
+    rc = lib.nvs_paged_attention(P, 1024, 128, P, P, 0, None, None, P, P, P, 8, 1, 1, 1, 256,
+                                 5, 2, 128, 256, 8, 0.125, P, 512, 128, None, 0, None)
+    assert rc == -1 and b"multiple of num_kv_heads" in lib.nvs_last_error()
+    rc = lib.nvs_paged_attention(P, 1024, 128, P, P, 3, None, None, P, P, P, 8, 1, 1, 1, 256,
+                                 4, 1, 128, 256, 8, 0.125, P, 512, 128, None, 0, None)
+    assert rc == -1 and b"k_scale" in lib.nvs_last_error()
+    rc = lib.nvs_paged_attention(P, 1024, 128, P, P, 0, None, None, P, P, P, 1, 1, 1, 1, 4096,
+                                 4, 1, 128, 256, 8, 0.125, P, 512, 128, None, 0, None)
+    assert rc == -1 and b"too short" in lib.nvs_last_error()
+    rc = lib.nvs_paged_attention(P, 1024, 128, P, P, 0, None, None, P, P, P, 32, 2, 2, 1, 4096,
+                                 4, 1, 128, 256, 8, 0.125, P, 512, 128, None, 0, None)
+    assert rc == -3 and b"workspace" in lib.nvs_last_error()
+    rc = lib.nvs_store_kvcache(P, P, 0, 1024, 128, 1024, 128, P, 4, P, P, 3, None, None, 8, 256,
+                               8, 128, None)
+    assert rc == -1 and b"k_scale" in lib.nvs_last_error()
+    rc = lib.nvs_store_kvcache(P, P, 0, 1024, 128, 1024, 128, P, 4, P, P, 0, None, None, 8, 256,
+                               8, 96, None)
+    assert rc == -2
+    assert lib.nvs_store_kvcache(P, P, 0, 8, 8, 8, 8, P, 0, P, P, 0, None, None, 8, 256, 8, 128, None) == 0
+
+
+def test_workspace_bytes():
+    lib = _lib.load()
+    assert lib.nvs_attention_workspace_bytes(64, 1, 256, 32, 8, 128, 256) == 0
+    n = lib.nvs_attention_workspace_bytes(64, 1, 8192, 32, 8, 128, 256)
+    assert n == 64 * 32 * 32 * 130 * 4
