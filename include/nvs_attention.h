@@ -135,8 +135,12 @@ int nvs_gather_kvcache(const void* k_cache, const void* v_cache,
                        uint8_t* kv_mask, void* stream);
 
 /*
- * Workspace (bytes) that nvs_paged_attention needs for the split-K decode
- * partials of a batch with these bounds.  0 is a valid answer.
+ * Workspace (bytes) that nvs_paged_attention / nvs_varlen_attention need for
+ * a batch with these bounds: the work plan the device builds from
+ * cu_seqlens (compact lists of decode partitions and prefill query tiles)
+ * followed by the split-K decode partials.  The workspace must be 256-byte
+ * aligned; it needs no initialisation and is scratch between calls; calls
+ * that share one workspace must be ordered on one stream.
  */
 int64_t nvs_attention_workspace_bytes(int num_seqs, int max_seqlen_q,
                                       int max_seqlen_k, int num_heads,
@@ -162,8 +166,9 @@ int64_t nvs_attention_workspace_bytes(int num_seqs, int max_seqlen_q,
  *   hq / (num_heads / num_kv_heads).
  *   cache_dtype   BF16, INT8 or FP8_E4M3 (scales required for the last two).
  *   out           [num_tokens, num_heads, head_dim] BF16.
- *   Rows with q_len == 1 run the split-K decode kernels and need `workspace`
- *   of at least nvs_attention_workspace_bytes(...) bytes.
+ *   Rows with q_len == 1 run the split-K decode kernels, the others the MFMA
+ *   prefill kernel; `workspace` holds at least
+ *   nvs_attention_workspace_bytes(...) bytes.
  *   head_dim must be 128; num_heads / num_kv_heads must be 1..16;
  *   block_size must be a multiple of 64.
  */
@@ -188,8 +193,8 @@ int nvs_paged_attention(const void* q, int64_t q_tok_stride,
  * no-prefix branch of prefill_torch (attention.py:400-439).
  *   k, v          [num_tokens, num_kv_heads, head_dim] BF16 with strides;
  *                 keys of sequence i are rows cu_seqlens_k[i] ..
- *                 cu_seqlens_k[i+1]-1.  Same mask, GQA map and output as
- *                 nvs_paged_attention; head_dim 128.
+ *                 cu_seqlens_k[i+1]-1.  Same mask, GQA map, output and
+ *                 workspace rule as nvs_paged_attention; head_dim 128.
  */
 int nvs_varlen_attention(const void* q, int64_t q_tok_stride,
                          int64_t q_head_stride, const void* k, const void* v,
@@ -201,6 +206,7 @@ int nvs_varlen_attention(const void* q, int64_t q_tok_stride,
                          int max_seqlen_k, int num_heads, int num_kv_heads,
                          int head_dim, float softmax_scale, void* out,
                          int64_t out_tok_stride, int64_t out_head_stride,
+                         void* workspace, int64_t workspace_bytes,
                          void* stream);
 
 #ifdef __cplusplus

@@ -23,15 +23,35 @@ static int validate_common(const AttnParams& P, const char* who) {
   return NVS_OK;
 }
 
+namespace nvs {
+static int prefill_tiles(int max_seqlen_q) {
+  const int t = (max_seqlen_q + kPrefillBM - 1) / kPrefillBM;
+  return t < 1 ? 1 : t;
+}
+
+int64_t attention_workspace_bytes(int num_seqs, int max_seqlen_q, int max_seqlen_k, int num_heads) {
+  if (num_seqs <= 0 || num_heads <= 0) return 0;
+  const int parts = decode_max_parts(max_seqlen_k);
+  return align256(plan_bytes(num_seqs, parts, prefill_tiles(max_seqlen_q))) +
+         decode_workspace_bytes(num_seqs, max_seqlen_k, num_heads);
+}
+}  // namespace nvs
+
 extern "C" int64_t nvs_attention_workspace_bytes(int num_seqs, int max_seqlen_q, int max_seqlen_k,
                                                  int num_heads, int num_kv_heads, int head_dim,
                                                  int block_size) {
-  (void)max_seqlen_q;
   (void)num_kv_heads;
   (void)head_dim;
   (void)block_size;
-  if (num_seqs <= 0 || num_heads <= 0) return 0;
-  return decode_workspace_bytes(num_seqs, max_seqlen_k, num_heads);
+  return attention_workspace_bytes(num_seqs, max_seqlen_q, max_seqlen_k, num_heads);
+}
+
+static int check_workspace(const AttnParams& P, const char* who) {
+  const int64_t need = attention_workspace_bytes(P.B, P.max_seqlen_q, P.max_seqlen_k, P.Hq);
+  NVS_REQUIRE(P.ws && P.ws_bytes >= need && ((uintptr_t)P.ws % 256) == 0, NVS_ERR_WORKSPACE,
+              "%s: workspace of %lld bytes (256-byte aligned) needed, %lld given", who,
+              (long long)need, (long long)P.ws_bytes);
+  return NVS_OK;
 }
 
 extern "C" int nvs_paged_attention(const void* q, int64_t q_tok_stride, int64_t q_head_stride,
@@ -70,15 +90,24 @@ extern "C" int nvs_paged_attention(const void* q, int64_t q_tok_stride, int64_t 
   NVS_REQUIRE(block_size > 0 && block_size % 64 == 0, NVS_ERR_UNSUPPORTED,
               "paged_attention: block_size must be a multiple of 64, got %d", block_size);
   NVS_REQUIRE(num_blocks > 0, NVS_ERR_INVALID, "paged_attention: empty cache");
+  NVS_REQUIRE(num_blocks < (1ll << 31) && bt_stride < (1ll << 31) &&
+                  (int64_t)num_seqs * bt_stride < (1ll << 31),
+              NVS_ERR_UNSUPPORTED, "paged_attention: block pool / block_tables too large");
   NVS_REQUIRE(bt_stride > 0 && ((int64_t)max_seqlen_k + block_size - 1) / block_size <= bt_stride,
               NVS_ERR_INVALID,
               "paged_attention: block_tables rows (%lld) too short for max_seqlen_k %d",
               (long long)bt_stride, max_seqlen_k);
   if (max_seqlen_q <= 0) return NVS_OK;
+  rc = check_workspace(P, "paged_attention");
+  if (rc != NVS_OK) return rc;
   hipStream_t s = (hipStream_t)stream;
-  rc = launch_decode(P, s);
+  const Plan plan = plan_at(workspace, num_seqs, decode_max_parts(max_seqlen_k), prefill_tiles(max_seqlen_q));
+  char* partials = (char*)workspace + align256(plan_bytes(num_seqs, plan.max_parts, plan.ntq));
+  rc = launch_plan(P, plan, /*paged=*/true, s);
+  if (rc != NVS_OK) return rc;
+  rc = launch_decode(P, plan, partials, s);
   if (rc != NVS_OK || max_seqlen_q == 1) return rc;
-  return launch_prefill(P, /*skip_decode_rows=*/true, s);
+  return launch_prefill(P, plan, s);
 }
 
 extern "C" int nvs_varlen_attention(const void* q, int64_t q_tok_stride, int64_t q_head_stride,
@@ -89,9 +118,10 @@ extern "C" int nvs_varlen_attention(const void* q, int64_t q_tok_stride, int64_t
                                     int max_seqlen_q, int max_seqlen_k, int num_heads,
                                     int num_kv_heads, int head_dim, float softmax_scale, void* out,
                                     int64_t out_tok_stride, int64_t out_head_stride,
-                                    void* stream) {
+                                    void* workspace, int64_t workspace_bytes, void* stream) {
   clear_error();
   AttnParams P = {};
+  P.ws = workspace; P.ws_bytes = workspace_bytes;
   P.q = q; P.q_ts = q_tok_stride; P.q_hs = q_head_stride;
   P.k = k; P.v = v; P.k_ts = k_tok_stride; P.k_hs = k_head_stride;
   P.v_ts = v_tok_stride; P.v_hs = v_head_stride;
@@ -110,5 +140,11 @@ extern "C" int nvs_varlen_attention(const void* q, int64_t q_tok_stride, int64_t
                   v_head_stride % 8 == 0 && ((uintptr_t)k % 16) == 0 && ((uintptr_t)v % 16) == 0,
               NVS_ERR_INVALID, "varlen_attention: k/v rows must be 16-byte aligned");
   if (max_seqlen_q <= 0) return NVS_OK;
-  return launch_prefill(P, /*skip_decode_rows=*/false, (hipStream_t)stream);
+  rc = check_workspace(P, "varlen_attention");
+  if (rc != NVS_OK) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  const Plan plan = plan_at(workspace, num_seqs, decode_max_parts(max_seqlen_k), prefill_tiles(max_seqlen_q));
+  rc = launch_plan(P, plan, /*paged=*/false, s);
+  if (rc != NVS_OK) return rc;
+  return launch_prefill(P, plan, s);
 }

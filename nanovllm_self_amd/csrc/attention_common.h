@@ -6,7 +6,18 @@
 namespace nvs {
 
 constexpr int kHeadDim = 128;    // head_dim served by the attention kernels
-constexpr int kDecodePart = 256; // keys per decode wave (one split-K partition)
+#ifndef NVS_DECODE_PART
+#define NVS_DECODE_PART 256
+#endif
+constexpr int kDecodePart = NVS_DECODE_PART;  // keys per decode wave (one split-K partition)
+#ifndef NVS_DECODE_BUFFERS
+#define NVS_DECODE_BUFFERS 2
+#endif
+constexpr int kDecodeBuffers = NVS_DECODE_BUFFERS;  // decode tile ring depth (>= 2)
+#ifndef NVS_DECODE_WAVES_PER_EU
+#define NVS_DECODE_WAVES_PER_EU 2
+#endif
+constexpr int kDecodeWavesPerEU = NVS_DECODE_WAVES_PER_EU;  // occupancy floor requested
 
 inline int decode_max_parts(int max_seqlen_k) {
   const int p = (max_seqlen_k + kDecodePart - 1) / kDecodePart;
@@ -41,9 +52,14 @@ __device__ __forceinline__ void code_pair_to_f32(uint32_t x, float& f0, float& f
 // in bf16, so no rounding happens.
 template <int KV, bool HI>
 __device__ __forceinline__ uint32_t code_pair_to_bf16x2(uint32_t x) {
-  float f0, f1;
-  code_pair_to_f32<KV, HI>(x, f0, f1);
-  return pack_exact_bf16x2(f0, f1);
+  if constexpr (KV == NVS_DTYPE_FP8_E4M3) {
+    // gfx950 converts two e4m3 codes straight to packed bf16 (scale 2^0).
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(x, 1.0f, HI));
+  } else {
+    float f0, f1;
+    code_pair_to_f32<KV, HI>(x, f0, f1);
+    return pack_exact_bf16x2(f0, f1);
+  }
 }
 
 // 8 codes (bytes of lo then hi) -> bf16x8 operand.
@@ -56,6 +72,56 @@ __device__ __forceinline__ bf16x8 codes8_to_bf16x8(uint32_t lo, uint32_t hi) {
   w[3] = code_pair_to_bf16x2<KV, true>(hi);
   return __builtin_bit_cast(bf16x8, w);
 }
+
+// ---------------------------------------------------------------------------
+// Work plan.  A one-work-group planning kernel turns cu_seqlens into compact
+// work lists in the workspace, so the attention kernels launch a fixed,
+// persistent grid and never dispatch empty work-groups (each costs the
+// dispatcher several nanoseconds; an upper-bound grid is mostly empty on
+// ragged batches).
+//   decode list:  b * max_parts + p, one entry per (q_len == 1 row, 256-key
+//                 partition); a row with no visible key gets one entry.
+//   prefill list: b * ntq + qt, one entry per (q_len > 1 row, 128-row query
+//                 tile), every row's tiles in descending qt (heaviest first).
+// ---------------------------------------------------------------------------
+constexpr int kPrefillBM = 128;  // query rows per prefill work item
+
+struct PlanHeader {
+  int n_decode;
+  int n_prefill;
+  int pad[62];  // keeps the lists 256-byte aligned
+};
+
+struct Plan {
+  PlanHeader* hdr;
+  int* dlist;
+  int* plist;
+  int max_parts;  // decode partitions per sequence (list stride)
+  int ntq;        // prefill query tiles per sequence (list stride)
+};
+
+inline int64_t align256(int64_t x) { return (x + 255) & ~(int64_t)255; }
+
+// Bytes of the plan for a batch; it sits at the start of the workspace.
+inline int64_t plan_bytes(int B, int max_parts, int ntq) {
+  return (int64_t)sizeof(PlanHeader) + align256((int64_t)B * max_parts * 4) +
+         align256((int64_t)B * ntq * 4);
+}
+
+inline Plan plan_at(void* ws, int B, int max_parts, int ntq) {
+  Plan p;
+  char* c = (char*)ws;
+  p.hdr = (PlanHeader*)c;
+  p.dlist = (int*)(c + sizeof(PlanHeader));
+  p.plist = (int*)(c + sizeof(PlanHeader) + align256((int64_t)B * max_parts * 4));
+  p.max_parts = max_parts;
+  p.ntq = ntq;
+  return p;
+}
+
+// Number of work-group slots the device runs at once for a kernel with
+// `per_cu` resident work-groups per CU (CU count cached per device).
+int device_slots(int per_cu);
 
 // Validated launch parameters of one attention call.
 struct AttnParams {
@@ -90,7 +156,9 @@ struct AttnParams {
 };
 
 int64_t decode_workspace_bytes(int num_seqs, int max_seqlen_k, int num_heads);
-int launch_decode(const AttnParams& P, hipStream_t stream);
-int launch_prefill(const AttnParams& P, bool skip_decode_rows, hipStream_t stream);
+int64_t attention_workspace_bytes(int num_seqs, int max_seqlen_q, int max_seqlen_k, int num_heads);
+int launch_plan(const AttnParams& P, const Plan& plan, bool paged, hipStream_t stream);
+int launch_decode(const AttnParams& P, const Plan& plan, void* partials, hipStream_t stream);
+int launch_prefill(const AttnParams& P, const Plan& plan, hipStream_t stream);
 
 }  // namespace nvs

@@ -17,7 +17,11 @@
 // codes are converted to bf16 exactly in registers (int8 and e4m3 values are
 // bf16-representable); the per-key scales multiply S (K) and P (V).
 // Each wave writes a partial (m, l, o[128]) per head; decode_reduce_kernel
-// merges the partitions with a log-sum-exp.
+// merges the partitions with a log-sum-exp (a second launch: the kernel
+// boundary makes the partials visible across XCDs without device-scope
+// fences, which on a multi-XCD part write back the L2).
+#include <algorithm>
+
 #include "nvs_common.h"
 #include "attention_common.h"
 
@@ -33,26 +37,30 @@ struct DecodeArgs {
   const int32_t* cu_q;
   const int32_t* cu_k;
   const int32_t* bt;
-  int64_t bt_stride;  // row stride == number of columns
-  int64_t NB;
-  int64_t T;  // query / output rows
+  int bt_stride;  // row stride == number of columns (32-bit: keeps the
+  int NB;         // block-table lookup a scalar compare + scalar load)
+  int64_t T;      // query / output rows
   int Hq, Hkv, g, bs;
   int max_parts;
   float scale_log2;
   float* ws_o;   // [B, Hq, max_parts, 128]
   float* ws_ml;  // [B, Hq, max_parts, 2]
+  Plan plan;
   uint16_t* out;
   int64_t out_ts, out_hs;
 };
 
-// Registers of one 32-key tile as loaded from HBM.
+// Registers of one 32-key tile as loaded from HBM.  `has` is false when the
+// tile's block-table entry is missing (< 0 or outside the pool); the loads
+// then read block 0 and the compute treats the keys as zero vectors.
 template <int KV>
 struct DecodeTile;
 
 template <>
 struct DecodeTile<NVS_DTYPE_BF16> {
-  u32x4 k[2][4];  // [subtile t][d step s]: key 16t + col, d = 32 grp + 8 s
+  u32x4 k[2][4];  // [subtile t][d step s]: key 16t + col, d = 32 s + 8 grp
   u32x4 v[8];     // [slot e]: key 16(e/4) + 4 grp + e%4, d = 8 col .. +7
+  bool has;
 };
 
 template <int KV>
@@ -61,72 +69,142 @@ struct DecodeTile {
   u32x2 v[8];     // [e]: 8 codes, d = 8 col .. +7
   float ksc[8];   // scales of the 8 keys the lane owns (slot order)
   float vsc[8];
+  bool has;
+};
+
+__device__ __forceinline__ int slot_key(int e, int grp) { return 16 * (e >> 2) + 4 * grp + (e & 3); }
+
+// head_dim elements of MFMA step s / lane group grp in the QK^T product:
+// d = kKStepStride * s + kKGroupStride * grp + 0..7.  Any split works as long
+// as K and Q use the same one; bf16 K uses d = 32 s + 8 grp so that one load
+// instruction reads 64 contiguous bytes of each of its 16 rows, code caches
+// keep d = 32 grp + 8 s (one 128-byte row per lane group pair of loads).
+template <int KV>
+constexpr int kKStepStride = (KV == NVS_DTYPE_BF16) ? 32 : 8;
+template <int KV>
+constexpr int kKGroupStride = (KV == NVS_DTYPE_BF16) ? 8 : 32;
+
+// Per-lane byte offsets from a tile's first row, identical for every tile:
+// loads take a wave-uniform 64-bit base (scalar registers) plus these 32-bit
+// lane offsets, so no per-load address arithmetic remains in the loop.
+struct LaneOffsets {
+  uint32_t k[2];   // key 16t + col, d = 8 grp (bf16) / 32 grp (codes)
+  uint32_t v[8];   // key slot_key(e), d = 8 col
+  uint32_t sc[8];  // scale of key slot_key(e)
 };
 
 template <int KV>
-__device__ __forceinline__ void decode_load(DecodeTile<KV>& T, const DecodeArgs& a, int b, int h,
-                                            int kt, int col, int grp) {
-  const int lblk = kt / a.bs;
-  int blk = lblk < a.bt_stride ? a.bt[(int64_t)b * a.bt_stride + lblk] : -1;
-  if (blk >= a.NB) blk = -1;  // never read outside the pool
-  const int64_t slot0 = (int64_t)blk * a.bs + (kt - lblk * a.bs);
-  constexpr int D = kHeadDim;
-  if (blk < 0) {
-    // Missing block: zero K and V (the eager path's zero padding).
-    if constexpr (KV == NVS_DTYPE_BF16) {
+__device__ __forceinline__ LaneOffsets lane_offsets(int Hkv, int col, int grp) {
+  constexpr uint32_t ESZ = (KV == NVS_DTYPE_BF16) ? 2 : 1;
+  const uint32_t row = (uint32_t)Hkv * kHeadDim * ESZ;  // bytes per token row (all heads)
+  LaneOffsets o;
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+  for (int t = 0; t < 2; ++t) o.k[t] = (uint32_t)(16 * t + col) * row + kKGroupStride<KV> * grp * ESZ;
 #pragma unroll
-        for (int s = 0; s < 4; ++s) T.k[t][s] = u32x4{0, 0, 0, 0};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) T.v[e] = u32x4{0, 0, 0, 0};
-    } else {
-#pragma unroll
-      for (int t = 0; t < 2; ++t) T.k[t][0] = T.k[t][1] = u32x4{0, 0, 0, 0};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        T.v[e] = u32x2{0, 0};
-        T.ksc[e] = 0.0f;
-        T.vsc[e] = 0.0f;
-      }
-    }
-    return;
+  for (int e = 0; e < 8; ++e) {
+    o.v[e] = (uint32_t)slot_key(e, grp) * row + 8 * col * ESZ;
+    o.sc[e] = (uint32_t)slot_key(e, grp) * Hkv * 4;
   }
+  return o;
+}
+
+// Block ids of the (at most kDecodePart / 64) blocks a partition spans,
+// looked up once when the wave starts, before any tile load is in flight: a
+// lookup between tile loads would have to wait for all of them.
+struct PartitionBlocks {
+  int lb0;       // logical block of the partition's first key
+  int id[kDecodePart / 64];
+};
+
+__device__ __forceinline__ PartitionBlocks partition_blocks(const DecodeArgs& a, int b, int kbeg, int kend) {
+  PartitionBlocks pb;
+  pb.lb0 = kbeg / a.bs;
+  const int lb1 = (kend - 1) / a.bs;
+#pragma unroll
+  for (int j = 0; j < kDecodePart / 64; ++j) {
+    const int lblk = pb.lb0 + j;
+    int blk = -1;
+    if (lblk <= lb1 && lblk < a.bt_stride) blk = a.bt[b * a.bt_stride + lblk];
+    pb.id[j] = __builtin_amdgcn_readfirstlane(blk);
+  }
+  return pb;
+}
+
+template <int KV>
+__device__ __forceinline__ void decode_load(DecodeTile<KV>& T, const DecodeArgs& a, const LaneOffsets& lo,
+                                            const PartitionBlocks& pb, int h, int kt) {
+  constexpr int ESZ = (KV == NVS_DTYPE_BF16) ? 2 : 1;
+  const int lblk = kt / a.bs;
+  const int j = lblk - pb.lb0;
+  int blk = pb.id[0];
+#pragma unroll
+  for (int i = 1; i < kDecodePart / 64; ++i) blk = (j == i) ? pb.id[i] : blk;
+  T.has = blk >= 0 && blk < a.NB;  // never read outside the pool
+  const int64_t row0 = ((int64_t)(T.has ? blk : 0) * a.bs + (kt - lblk * a.bs)) * a.Hkv + h;
+  const char* kb = (const char*)a.kc + row0 * kHeadDim * ESZ;
+  const char* vb = (const char*)a.vc + row0 * kHeadDim * ESZ;
   if constexpr (KV == NVS_DTYPE_BF16) {
-    const uint16_t* kc = (const uint16_t*)a.kc;
-    const uint16_t* vc = (const uint16_t*)a.vc;
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const uint16_t* kr = kc + ((slot0 + 16 * t + col) * a.Hkv + h) * D + 32 * grp;
+    for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int s = 0; s < 4; ++s) T.k[t][s] = *reinterpret_cast<const u32x4*>(kr + 8 * s);
-    }
+      for (int s = 0; s < 4; ++s) T.k[t][s] = *reinterpret_cast<const u32x4*>(kb + lo.k[t] + 64 * s);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int key = 16 * (e >> 2) + 4 * grp + (e & 3);
-      T.v[e] = *reinterpret_cast<const u32x4*>(vc + ((slot0 + key) * a.Hkv + h) * D + 8 * col);
-    }
+    for (int e = 0; e < 8; ++e) T.v[e] = *reinterpret_cast<const u32x4*>(vb + lo.v[e]);
   } else {
-    const uint8_t* kc = (const uint8_t*)a.kc;
-    const uint8_t* vc = (const uint8_t*)a.vc;
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      const uint8_t* kr = kc + ((slot0 + 16 * t + col) * a.Hkv + h) * D + 32 * grp;
-      T.k[t][0] = *reinterpret_cast<const u32x4*>(kr);
-      T.k[t][1] = *reinterpret_cast<const u32x4*>(kr + 16);
+      T.k[t][0] = *reinterpret_cast<const u32x4*>(kb + lo.k[t]);
+      T.k[t][1] = *reinterpret_cast<const u32x4*>(kb + lo.k[t] + 16);
     }
+    const char* ksb = (const char*)(a.ks + row0);
+    const char* vsb = (const char*)(a.vs + row0);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const int key = 16 * (e >> 2) + 4 * grp + (e & 3);
-      const int64_t row = (slot0 + key) * a.Hkv + h;
-      T.v[e] = *reinterpret_cast<const u32x2*>(vc + row * D + 8 * col);
-      T.ksc[e] = a.ks[row];
-      T.vsc[e] = a.vs[row];
+      T.v[e] = *reinterpret_cast<const u32x2*>(vb + lo.v[e]);
+      T.ksc[e] = *reinterpret_cast<const float*>(ksb + lo.sc[e]);
+      T.vsc[e] = *reinterpret_cast<const float*>(vsb + lo.sc[e]);
     }
   }
 }
 
+// A missing block reads as all-zero keys and values: clear the tile in place
+// (the loads fetched block 0).
 template <int KV>
+__device__ __forceinline__ void zero_tile(DecodeTile<KV>& T) {
+  if constexpr (KV == NVS_DTYPE_BF16) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) T.k[t][s] = u32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) T.v[e] = u32x4{0, 0, 0, 0};
+  } else {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) T.k[t][0] = T.k[t][1] = u32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      T.v[e] = u32x2{0, 0};
+      T.ksc[e] = 0.0f;
+      T.vsc[e] = 0.0f;
+    }
+  }
+}
+
+// v_perm_b32 selector bytes >= 0x0C produce 0x00: masked slots are zeroed
+// inside the transpose instead of by copying registers.
+__device__ __forceinline__ uint32_t masked_sel(uint32_t sel, uint32_t keep) {
+  return (sel & keep) | (0x0c0c0c0cu & ~keep);
+}
+
+// The running max is only moved (and O, l rescaled) when a tile raises it by
+// more than 2^kLazyRescale: until then p = 2^(s - m) stays below 2^8, which
+// bf16 P and the fp32 accumulators carry exactly as well.
+constexpr float kLazyRescale = 8.0f;
+
+// MASKED: the partition's last tile; keys outside [kt, kend) are masked (score
+// -inf, value slot zeroed inside the transpose so stale cache contents can
+// never reach the sum).
+template <int KV, bool MASKED>
 __device__ __forceinline__ void decode_tile_compute(const DecodeTile<KV>& T, const bf16x8 (&qop)[4],
                                                     f32x4 (&o)[8], float& m_run, float& l_run,
                                                     int kt, int kend, int grp, float scale_log2) {
@@ -148,17 +226,16 @@ __device__ __forceinline__ void decode_tile_compute(const DecodeTile<KV>& T, con
     }
   }
   // ---- online softmax (log2 domain) -----------------------------------------
-  const bool partial = kt + 32 > kend;
+  bool valid[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) valid[e] = !MASKED || (kt + slot_key(e, grp) < kend);
   float sv[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     float f = scale_log2;
     if constexpr (KV != NVS_DTYPE_BF16) f *= T.ksc[e];
     float x = s[e >> 2][e & 3] * f;
-    if (partial) {
-      const int key = kt + 16 * (e >> 2) + 4 * grp + (e & 3);
-      x = key < kend ? x : -INFINITY;
-    }
+    if constexpr (MASKED) x = valid[e] ? x : -INFINITY;  // outside the partition
     sv[e] = x;
   }
   float mt = sv[0];
@@ -166,19 +243,22 @@ __device__ __forceinline__ void decode_tile_compute(const DecodeTile<KV>& T, con
   for (int e = 1; e < 8; ++e) mt = fmaxf(mt, sv[e]);
   mt = fmaxf(mt, shfl_xor(mt, 16));
   mt = fmaxf(mt, shfl_xor(mt, 32));
-  const float m_new = fmaxf(m_run, mt);
-  const float alpha = fast_exp2(m_run - m_new);
-  m_run = m_new;
-  l_run *= alpha;
+  if (__any(mt > m_run + kLazyRescale)) {
+    const float m_new = fmaxf(m_run, mt);
+    const float alpha = fast_exp2(m_run - m_new);
+    m_run = m_new;
+    l_run *= alpha;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) o[j] *= alpha;
+    for (int j = 0; j < 8; ++j) o[j] *= alpha;
+  }
   float pv[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const float p = fast_exp2(sv[e] - m_new);
+    const float p = fast_exp2(sv[e] - m_run);
     l_run += p;
     float pw = p;
-    if constexpr (KV != NVS_DTYPE_BF16) pw = (sv[e] == -INFINITY) ? 0.0f : p * T.vsc[e];
+    if constexpr (KV != NVS_DTYPE_BF16) pw = p * T.vsc[e];
+    if constexpr (MASKED) pw = valid[e] ? pw : 0.0f;
     pv[e] = pw;
   }
   u32x4 pw;
@@ -187,38 +267,28 @@ __device__ __forceinline__ void decode_tile_compute(const DecodeTile<KV>& T, con
   const bf16x8 pop = __builtin_bit_cast(bf16x8, pw);
 
   // ---- V^T operands (transpose in registers) and O^T += V^T . P^T ---------
+  uint32_t keep[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const bool v0 = valid[2 * m], v1 = valid[2 * m + 1];
+    if constexpr (KV == NVS_DTYPE_BF16)
+      keep[m] = (v0 ? 0x0000ffffu : 0u) | (v1 ? 0xffff0000u : 0u);
+    else
+      keep[m] = (v0 ? 0x00ff00ffu : 0u) | (v1 ? 0xff00ff00u : 0u);
+  }
   if constexpr (KV == NVS_DTYPE_BF16) {
-    u32x4 v[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = T.v[e];
-    if (partial) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int key = kt + 16 * (e >> 2) + 4 * grp + (e & 3);
-        if (key >= kend) v[e] = u32x4{0, 0, 0, 0};
-      }
-    }
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
       u32x4 aw;
 #pragma unroll
       for (int m = 0; m < 4; ++m)
-        aw[m] = __builtin_amdgcn_perm(v[2 * m + 1][j >> 1], v[2 * m][j >> 1], sel);
+        aw[m] = __builtin_amdgcn_perm(T.v[2 * m + 1][j >> 1], T.v[2 * m][j >> 1],
+                                      MASKED ? masked_sel(sel, keep[m]) : sel);
       o[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, aw), pop, o[j], 0,
                                                      0, 0);
     }
   } else {
-    u32x2 v[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = T.v[e];
-    if (partial) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int key = kt + 16 * (e >> 2) + 4 * grp + (e & 3);
-        if (key >= kend) v[e] = u32x2{0, 0};
-      }
-    }
 #pragma unroll
     for (int jp = 0; jp < 4; ++jp) {  // d pair (2jp, 2jp+1) within the lane's 8
       const int wsel = jp >> 1;        // code word holding bytes 2jp, 2jp+1
@@ -229,7 +299,8 @@ __device__ __forceinline__ void decode_tile_compute(const DecodeTile<KV>& T, con
       u32x4 a0, a1;
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
-        const uint32_t x = __builtin_amdgcn_perm(v[2 * m + 1][wsel], v[2 * m][wsel], sel);
+        const uint32_t x = __builtin_amdgcn_perm(T.v[2 * m + 1][wsel], T.v[2 * m][wsel],
+                                                 MASKED ? masked_sel(sel, keep[m]) : sel);
         a0[m] = code_pair_to_bf16x2<KV, false>(x);
         a1[m] = code_pair_to_bf16x2<KV, true>(x);
       }
@@ -241,24 +312,47 @@ __device__ __forceinline__ void decode_tile_compute(const DecodeTile<KV>& T, con
   }
 }
 
-template <int KV>
-__global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
-  const int p = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int s = 32; s >= 1; s >>= 1) v = fmaxf(v, shfl_xor(v, s));
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int s = 32; s >= 1; s >>= 1) v += shfl_xor(v, s);
+  return v;
+}
+
+// One work item: (decode sequence b, kv head h, partition p).
+template <int KV, int NBUF>
+__device__ __forceinline__ void paged_decode_item(const DecodeArgs& a, int b, int h, int p) {
   const int lane = threadIdx.x;
   const int q0 = a.cu_q[b];
-  if (a.cu_q[b + 1] - q0 != 1 || q0 < 0 || q0 >= a.T) return;
   const int klen = a.cu_k[b + 1] - a.cu_k[b];
   const int kbeg = p * kDecodePart;
-  if (kbeg >= klen) return;
+  if (kbeg >= klen) {
+    if (p == 0 && a.max_parts == 1) {  // no visible key: output 0 (the merge handles max_parts > 1)
+      for (int i = lane; i < a.g * (kHeadDim / 2); i += 64) {
+        const int c = i / (kHeadDim / 2), d = 2 * (i % (kHeadDim / 2));
+        *reinterpret_cast<uint32_t*>(a.out + (int64_t)q0 * a.out_ts + (int64_t)(h * a.g + c) * a.out_hs + d) = 0u;
+      }
+    }
+    return;
+  }
   const int kend = min(kbeg + kDecodePart, klen);
+  const int ntiles = (kend - kbeg + 31) >> 5;
   const int col = lane & 15, grp = lane >> 4;
 
-  // Q^T as the B operand: column = head (col < g), d = 32 grp + 8 s .. +7.
+  // Q^T as the B operand: column = head (col < g); step s, lane group grp
+  // holds the same 8 d values as the K operand: d = 32 s + 8 grp for bf16
+  // caches, 32 grp + 8 s for code caches.
   bf16x8 qop[4];
   if (col < a.g) {
-    const uint16_t* qp = a.q + (int64_t)q0 * a.q_ts + (int64_t)(h * a.g + col) * a.q_hs + 32 * grp;
+    const uint16_t* qp = a.q + (int64_t)q0 * a.q_ts + (int64_t)(h * a.g + col) * a.q_hs +
+                         kKGroupStride<KV> * grp;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) qop[s] = *reinterpret_cast<const bf16x8*>(qp + 8 * s);
+    for (int s = 0; s < 4; ++s) qop[s] = *reinterpret_cast<const bf16x8*>(qp + kKStepStride<KV> * s);
   } else {
 #pragma unroll
     for (int s = 0; s < 4; ++s) qop[s] = __builtin_bit_cast(bf16x8, u32x4{0, 0, 0, 0});
@@ -269,24 +363,54 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
   for (int j = 0; j < 8; ++j) o[j] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.0f;
 
-  DecodeTile<KV> ta, tb;
-  decode_load<KV>(ta, a, b, h, kbeg, col, grp);
-  for (int kt = kbeg; kt < kend; kt += 64) {
-    const bool two = kt + 32 < kend;
-    if (two) decode_load<KV>(tb, a, b, h, kt + 32, col, grp);
-    decode_tile_compute<KV>(ta, qop, o, m_run, l_run, kt, kend, grp, a.scale_log2);
-    if (!two) break;
-    if (kt + 64 < kend) decode_load<KV>(ta, a, b, h, kt + 64, col, grp);
-    decode_tile_compute<KV>(tb, qop, o, m_run, l_run, kt + 32, kend, grp, a.scale_log2);
+  // Ring of NBUF tiles, fully unrolled over the partition so every buffer
+  // index is a compile-time constant: NBUF - 1 tiles are in flight while one
+  // is consumed.
+  // The scheduling barriers keep each tile's loads in issue order: the
+  // hardware's load counter retires in order, so a later tile's load hoisted
+  // above an earlier one would make the wait for the earlier tile drain it too.
+  // Loads are issued unconditionally (tiles past the end re-read the last
+  // tile, an L2 hit) so that every path issues the same loads in the same
+  // order and each wait covers exactly the tile about to be used.
+  constexpr int NT = kDecodePart / 32;
+  const LaneOffsets lo = lane_offsets<KV>(a.Hkv, col, grp);
+  const PartitionBlocks pb = partition_blocks(a, b, kbeg, kend);
+  DecodeTile<KV> ring[NBUF];
+  const int last = ntiles - 1;
+#pragma unroll
+  for (int i = 0; i < NBUF - 1; ++i) {
+    decode_load<KV>(ring[i], a, lo, pb, h, kbeg + 32 * min(i, last));
+    __builtin_amdgcn_sched_barrier(0);
+  }
+#pragma unroll
+  for (int i = 0; i < NT; ++i) {
+    if (i + NBUF - 1 < NT)
+      decode_load<KV>(ring[(i + NBUF - 1) % NBUF], a, lo, pb, h, kbeg + 32 * min(i + NBUF - 1, last));
+    __builtin_amdgcn_sched_barrier(0);
+    if (i < last) {  // every tile but the last is full: no masking
+      if (!ring[i % NBUF].has) zero_tile(ring[i % NBUF]);
+      decode_tile_compute<KV, false>(ring[i % NBUF], qop, o, m_run, l_run, kbeg + 32 * i, kend, grp,
+                                     a.scale_log2);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // The last tile (possibly partial) runs the masked path; its ring slot is
+  // last % NBUF (later clamped loads only re-read the same tile).
+#pragma unroll
+  for (int r = 0; r < NBUF; ++r) {
+    if (last % NBUF == r) {
+      if (!ring[r].has) zero_tile(ring[r]);
+      decode_tile_compute<KV, true>(ring[r], qop, o, m_run, l_run, kbeg + 32 * last, kend, grp,
+                                    a.scale_log2);
+    }
   }
   l_run += shfl_xor(l_run, 16);
   l_run += shfl_xor(l_run, 32);
 
-  if (col < a.g) {
-    const int hq = h * a.g + col;
-    // Lane (col, grp) holds O[hq][d] for d = 32 grp + 8 r + j.
-    if (a.max_parts == 1) {
-      // Single partition: finish here.
+  if (a.max_parts == 1) {
+    // Single partition: normalise and write the output here.
+    if (col < a.g) {
+      const int hq = h * a.g + col;
       const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
       uint16_t* op = a.out + (int64_t)q0 * a.out_ts + (int64_t)hq * a.out_hs + 32 * grp;
 #pragma unroll
@@ -296,44 +420,86 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
         for (int m = 0; m < 4; ++m) w[m] = pack_bf16x2(o[2 * m][r] * inv, o[2 * m + 1][r] * inv);
         *reinterpret_cast<u32x4*>(op + 8 * r) = w;
       }
-    } else {
-      const int64_t base = ((int64_t)b * a.Hq + hq) * a.max_parts + p;
-      float* op = a.ws_o + base * kHeadDim + 32 * grp;
+    }
+    return;
+  }
+  // Lane (col, grp) holds O[hq][d] for d = 32 grp + 8 r + j.
+  if (col < a.g) {
+    const int hq = h * a.g + col;
+    const int64_t base = ((int64_t)b * a.Hq + hq) * a.max_parts + p;
+    float* op = a.ws_o + base * kHeadDim + 32 * grp;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        *reinterpret_cast<f32x4*>(op + 8 * r) = f32x4{o[0][r], o[1][r], o[2][r], o[3][r]};
-        *reinterpret_cast<f32x4*>(op + 8 * r + 4) = f32x4{o[4][r], o[5][r], o[6][r], o[7][r]};
-      }
-      if (grp == 0) {
-        a.ws_ml[base * 2] = m_run;
-        a.ws_ml[base * 2 + 1] = l_run;
-      }
+    for (int r = 0; r < 4; ++r) {
+      *reinterpret_cast<f32x4*>(op + 8 * r) = f32x4{o[0][r], o[1][r], o[2][r], o[3][r]};
+      *reinterpret_cast<f32x4*>(op + 8 * r + 4) = f32x4{o[4][r], o[5][r], o[6][r], o[7][r]};
+    }
+    if (grp == 0) {
+      a.ws_ml[base * 2] = m_run;
+      a.ws_ml[base * 2 + 1] = l_run;
     }
   }
 }
 
-// Merge the partitions of every (decode sequence, query head).
-// 64 threads, each owning 2 of the 128 head_dim elements.
+// Persistent: each wave walks the plan's decode list with a grid stride, kv
+// head fastest, so the Hkv waves reading one block's rows run side by side.
+template <int KV>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kDecodeWavesPerEU)))
+void paged_decode_kernel(DecodeArgs a) {
+  const int total = a.plan.hdr->n_decode * a.Hkv;
+  for (int k = blockIdx.x; k < total; k += gridDim.x) {
+    const int idx = k / a.Hkv;
+    const int h = k - idx * a.Hkv;
+    const int item = __builtin_amdgcn_readfirstlane(a.plan.dlist[idx]);
+    const int b = item / a.max_parts;
+    paged_decode_item<KV, kDecodeBuffers>(a, b, h, item - b * a.max_parts);
+  }
+}
+
+// Log-sum-exp merge of the partitions of every (decode sequence, query
+// head); one wave each.  Lane l owns head_dim elements 2l, 2l + 1.  Partition
+// weights are computed lane-parallel and broadcast with a shuffle, and the
+// partial-output loads are unrolled so many are in flight at once.
 __global__ __launch_bounds__(64) void decode_reduce_kernel(DecodeArgs a) {
   const int hq = blockIdx.x, b = blockIdx.y;
+  const int lane = threadIdx.x;
   const int q0 = a.cu_q[b];
   if (a.cu_q[b + 1] - q0 != 1 || q0 < 0 || q0 >= a.T) return;
   const int klen = a.cu_k[b + 1] - a.cu_k[b];
   const int parts = klen > 0 ? min((klen + kDecodePart - 1) / kDecodePart, a.max_parts) : 0;
-  const int d = 2 * threadIdx.x;
   const int64_t base = ((int64_t)b * a.Hq + hq) * a.max_parts;
+  const float* ml = a.ws_ml + base * 2;
   float M = -INFINITY;
-  for (int p = 0; p < parts; ++p) M = fmaxf(M, a.ws_ml[(base + p) * 2]);
-  float L = 0.0f, acc0 = 0.0f, acc1 = 0.0f;
-  for (int p = 0; p < parts; ++p) {
-    const float w = fast_exp2(a.ws_ml[(base + p) * 2] - M);
-    L += w * a.ws_ml[(base + p) * 2 + 1];
-    const float2 ov = *reinterpret_cast<const float2*>(a.ws_o + (base + p) * kHeadDim + d);
-    acc0 += w * ov.x;
-    acc1 += w * ov.y;
+  for (int p = lane; p < parts; p += 64) M = fmaxf(M, ml[2 * p]);
+  M = wave_max(M);
+  float L = 0.0f;
+  for (int p = lane; p < parts; p += 64) L += fast_exp2(ml[2 * p] - M) * ml[2 * p + 1];
+  L = wave_sum(L);
+  const float* po = a.ws_o + base * kHeadDim + 2 * lane;
+  float acc0 = 0.0f, acc1 = 0.0f;
+  for (int p0 = 0; p0 < parts; p0 += 64) {
+    const int n = min(64, parts - p0);
+    const float wl = lane < n ? fast_exp2(ml[2 * (p0 + lane)] - M) : 0.0f;
+    int i = 0;
+    for (; i + 8 <= n; i += 8) {
+      float2 ov[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) ov[u] = *reinterpret_cast<const float2*>(po + (int64_t)(p0 + i + u) * kHeadDim);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const float w = __shfl(wl, i + u, 64);
+        acc0 += w * ov[u].x;
+        acc1 += w * ov[u].y;
+      }
+    }
+    for (; i < n; ++i) {
+      const float w = __shfl(wl, i, 64);
+      const float2 ov = *reinterpret_cast<const float2*>(po + (int64_t)(p0 + i) * kHeadDim);
+      acc0 += w * ov.x;
+      acc1 += w * ov.y;
+    }
   }
   const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-  uint16_t* op = a.out + (int64_t)q0 * a.out_ts + (int64_t)hq * a.out_hs + d;
+  uint16_t* op = a.out + (int64_t)q0 * a.out_ts + (int64_t)hq * a.out_hs + 2 * lane;
   *reinterpret_cast<uint32_t*>(op) = pack_bf16x2(acc0 * inv, acc1 * inv);
 }
 
@@ -343,25 +509,25 @@ int64_t decode_workspace_bytes(int num_seqs, int max_seqlen_k, int num_heads) {
   return (int64_t)num_seqs * num_heads * parts * (kHeadDim + 2) * (int64_t)sizeof(float);
 }
 
-int launch_decode(const AttnParams& P, hipStream_t stream) {
+int launch_decode(const AttnParams& P, const Plan& plan, void* partials, hipStream_t stream) {
   DecodeArgs a;
   a.q = (const uint16_t*)P.q; a.q_ts = P.q_ts; a.q_hs = P.q_hs;
   a.kc = P.kc; a.vc = P.vc; a.ks = P.ks; a.vs = P.vs;
-  a.cu_q = P.cu_q; a.cu_k = P.cu_k; a.bt = P.bt; a.bt_stride = P.bt_stride; a.NB = P.NB; a.T = P.T;
+  a.cu_q = P.cu_q; a.cu_k = P.cu_k; a.bt = P.bt; a.bt_stride = (int)P.bt_stride; a.NB = (int)P.NB; a.T = P.T;
   a.Hq = P.Hq; a.Hkv = P.Hkv; a.g = P.Hq / P.Hkv; a.bs = P.bs;
-  a.max_parts = decode_max_parts(P.max_seqlen_k);
+  a.max_parts = plan.max_parts;
   a.scale_log2 = P.softmax_scale * 1.4426950408889634f;
   a.out = (uint16_t*)P.out; a.out_ts = P.out_ts; a.out_hs = P.out_hs;
+  a.plan = plan;
   a.ws_o = nullptr; a.ws_ml = nullptr;
   if (a.max_parts > 1) {
-    const int64_t need = decode_workspace_bytes(P.B, P.max_seqlen_k, P.Hq);
-    NVS_REQUIRE(P.ws && P.ws_bytes >= need, NVS_ERR_WORKSPACE,
-                "paged_attention: decode workspace of %lld bytes needed, %lld given",
-                (long long)need, (long long)P.ws_bytes);
-    a.ws_o = (float*)P.ws;
+    a.ws_o = (float*)partials;
     a.ws_ml = a.ws_o + (int64_t)P.B * P.Hq * a.max_parts * kHeadDim;
   }
-  dim3 grid(a.max_parts, P.Hkv, P.B), block(64);
+  // One wave per SIMD slot (2 per SIMD), never more than the items that can exist.
+  const int64_t upper = (int64_t)P.B * a.max_parts * P.Hkv;
+  const int waves = (int)std::min<int64_t>(upper, device_slots(4 * kDecodeWavesPerEU));
+  dim3 grid(waves), block(64);
   switch (P.cache_dtype) {
     case NVS_DTYPE_BF16:
       hipLaunchKernelGGL(paged_decode_kernel<NVS_DTYPE_BF16>, grid, block, 0, stream, a);

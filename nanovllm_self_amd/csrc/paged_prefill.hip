@@ -22,12 +22,14 @@
 // Scheduling: work-groups are dispatched longest-first (last query tiles of
 // every sequence first) and the g query heads that share a kv head land on
 // the same XCD so their K/V tiles are fetched into that XCD's L2 once.
+#include <algorithm>
+
 #include "nvs_common.h"
 #include "attention_common.h"
 
 namespace nvs {
 
-constexpr int kBM = 128;       // query rows per work-group
+constexpr int kBM = kPrefillBM;  // query rows per work item
 constexpr int kBN = 64;        // keys per tile
 constexpr int kKStride = 136;  // bf16 per K row in LDS (272 B: conflict-free b128 reads)
 constexpr int kVStride = 68;   // bf16 per V^T row in LDS (136 B: conflict-free b64 access)
@@ -40,8 +42,8 @@ struct PrefillArgs {
   const float* ks;
   const float* vs;
   const int32_t* bt;
-  int64_t bt_stride;  // row stride == number of columns
-  int64_t NB;
+  int bt_stride;      // row stride == number of columns (32-bit: scalar lookup)
+  int NB;
   int64_t T;          // rows of the local k/v
   int bs;
   const uint16_t* k;
@@ -49,8 +51,8 @@ struct PrefillArgs {
   int64_t k_ts, k_hs, v_ts, v_hs;
   const int32_t* cu_q;
   const int32_t* cu_k;
-  int B, Hq, Hkv, g, ntq, units;
-  int skip_decode;
+  int B, Hq, Hkv, g;
+  Plan plan;
   float scale_log2;
   uint16_t* out;
   int64_t out_ts, out_hs;
@@ -83,7 +85,7 @@ __device__ __forceinline__ void prefill_fill_load(FillRegs<KV>& R, const Prefill
   bool have = true;
   if constexpr (PAGED) {
     const int lblk = kt / a.bs;
-    const int blk = lblk < a.bt_stride ? a.bt[(int64_t)b * a.bt_stride + lblk] : -1;
+    const int blk = lblk < a.bt_stride ? a.bt[b * a.bt_stride + lblk] : -1;
     have = blk >= 0 && blk < a.NB;  // never read outside the pool
     slot0 = (int64_t)blk * a.bs + (kt - lblk * a.bs);
   }
@@ -185,26 +187,14 @@ __device__ __forceinline__ void prefill_fill_store(const FillRegs<KV>& R, uint16
   }
 }
 
+// One work item: (sequence b, query tile qt, query head hkv * g + cg).  Every
+// thread of the work-group runs the same items, so the barriers inside match.
 template <int KV, bool PAGED>
-__global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[kBN * kKStride];
-  __shared__ __attribute__((aligned(16))) uint16_t Vt[kHeadDim * kVStride];
-
-  // Work item: hw id -> (unit u, head-in-group c) with unit u on XCD u % 8.
-  const int hw = blockIdx.x;
-  const int xcd = hw & 7, r8 = hw >> 3;
-  const int cg = r8 % a.g;
-  const int u = 8 * (r8 / a.g) + xcd;
-  if (u >= a.units) return;
-  const int hkv = u % a.Hkv;
-  const int ub = u / a.Hkv;
-  const int b = ub % a.B;
-  const int qt = a.ntq - 1 - ub / a.B;
+__device__ __forceinline__ void prefill_item(const PrefillArgs& a, int b, int qt, int hkv, int cg,
+                                             uint16_t* Ks, uint16_t* Vt) {
   const int hq = hkv * a.g + cg;
   const int q0 = a.cu_q[b];
   const int L = a.cu_q[b + 1] - q0;
-  if (PAGED && a.skip_decode && L == 1) return;
-  if (q0 < 0 || (int64_t)q0 + L > a.T) return;  // malformed cu_seqlens_q: never touch rows past T
   const int m0 = qt * kBM;
   if (m0 >= L) return;
   const int k0 = a.cu_k[b];
@@ -353,26 +343,46 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
   }
 }
 
-int launch_prefill(const AttnParams& P, bool skip_decode_rows, hipStream_t stream) {
+// Persistent: each work-group walks the plan's prefill list.  Work k maps to
+// (unit u, head-in-group c) with u = (list index, kv head) and k % 8 == u % 8,
+// so with a grid that is a multiple of 8 the g query heads of a unit run on
+// one XCD and fetch its K/V tiles into that XCD's L2 once.
+template <int KV, bool PAGED>
+__global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[kBN * kKStride];
+  __shared__ __attribute__((aligned(16))) uint16_t Vt[kHeadDim * kVStride];
+  const int units = a.plan.hdr->n_prefill * a.Hkv;
+  const int total = ((units + 7) / 8) * 8 * a.g;
+  for (int k = blockIdx.x; k < total; k += gridDim.x) {
+    const int xcd = k & 7, r8 = k >> 3;
+    const int cg = r8 % a.g;
+    const int u = 8 * (r8 / a.g) + xcd;
+    if (u >= units) continue;
+    const int idx = u / a.Hkv;
+    const int hkv = u - idx * a.Hkv;
+    const int item = __builtin_amdgcn_readfirstlane(a.plan.plist[idx]);
+    const int b = item / a.plan.ntq;
+    prefill_item<KV, PAGED>(a, b, item - b * a.plan.ntq, hkv, cg, Ks, Vt);
+  }
+}
+
+int launch_prefill(const AttnParams& P, const Plan& plan, hipStream_t stream) {
   PrefillArgs a;
   a.q = (const uint16_t*)P.q; a.q_ts = P.q_ts; a.q_hs = P.q_hs;
   a.kc = P.kc; a.vc = P.vc; a.ks = P.ks; a.vs = P.vs;
-  a.bt = P.bt; a.bt_stride = P.bt_stride; a.bs = P.bs; a.NB = P.NB; a.T = P.T;
+  a.bt = P.bt; a.bt_stride = (int)P.bt_stride; a.bs = P.bs; a.NB = (int)P.NB; a.T = P.T;
   a.k = (const uint16_t*)P.k; a.v = (const uint16_t*)P.v;
   a.k_ts = P.k_ts; a.k_hs = P.k_hs; a.v_ts = P.v_ts; a.v_hs = P.v_hs;
   a.cu_q = P.cu_q; a.cu_k = P.cu_k;
   a.B = P.B; a.Hq = P.Hq; a.Hkv = P.Hkv; a.g = P.Hq / P.Hkv;
-  a.ntq = (P.max_seqlen_q + kBM - 1) / kBM;
-  a.skip_decode = skip_decode_rows ? 1 : 0;
+  a.plan = plan;
   a.scale_log2 = P.softmax_scale * 1.4426950408889634f;
   a.out = (uint16_t*)P.out; a.out_ts = P.out_ts; a.out_hs = P.out_hs;
-  if (a.ntq <= 0 || P.B <= 0) return NVS_OK;
-  const int64_t units = (int64_t)a.ntq * P.B * P.Hkv;
-  NVS_REQUIRE(units < (1ll << 28), NVS_ERR_INVALID, "prefill: too many work items");
-  a.units = (int)units;
-  const int64_t groups8 = (units + 7) / 8;
-  const int64_t wgs = groups8 * 8 * a.g;
-  NVS_REQUIRE(wgs < (1ll << 31), NVS_ERR_INVALID, "prefill: grid too large");
+  if (plan.ntq <= 0 || P.B <= 0) return NVS_OK;
+  // One work-group per CU (a multiple of 8), never more than the work there can be.
+  const int64_t upper = (((int64_t)P.B * plan.ntq * P.Hkv + 7) / 8) * 8 * a.g;
+  int64_t wgs = std::min<int64_t>(upper, (int64_t)device_slots(1));
+  wgs = std::max<int64_t>(8, wgs & ~(int64_t)7);
   dim3 grid((unsigned)wgs), block(256);
   const bool paged = P.bt != nullptr;
   if (!paged) {

@@ -37,7 +37,9 @@ def _need_device(t: torch.Tensor, what: str) -> None:
 
 
 def attention_workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
-    """Per-device split-K workspace, grown on demand (never inside graph capture)."""
+    """Per-device split-K workspace, grown on demand (never inside graph capture).
+
+    Calls that share it must be ordered on one stream."""
     if nbytes <= 0:
         return None
     key = torch.device(device)
@@ -53,9 +55,11 @@ def attention_workspace(device: torch.device, nbytes: int) -> torch.Tensor | Non
     return buf
 
 
-def reserve_attention_workspace(num_seqs: int, max_seqlen_k: int, num_heads: int, device) -> None:
-    """Pre-size the workspace for batches up to these bounds."""
-    n = _lib.load().nvs_attention_workspace_bytes(num_seqs, 1, max_seqlen_k, num_heads, 0, 128, 0)
+def reserve_attention_workspace(num_seqs: int, max_seqlen_q: int, max_seqlen_k: int, num_heads: int,
+                                device) -> None:
+    """Pre-size the workspace for batches up to these bounds (for example
+    before capturing a graph, where it cannot grow)."""
+    n = _lib.load().nvs_attention_workspace_bytes(num_seqs, max_seqlen_q, max_seqlen_k, num_heads, 0, 128, 0)
     attention_workspace(torch.device(device), int(n))
 
 
@@ -262,6 +266,10 @@ class PagedAttention(nn.Module):
         scale = 1.0 / math.sqrt(self.head_dim)
         lib = _lib.load()
         stream = _lib.stream_of(q)
+        max_q, max_k = int(context.max_seqlen_q), int(context.max_seqlen_k)
+        ws_bytes = int(lib.nvs_attention_workspace_bytes(
+            B, max_q, max_k, self.num_heads, self.num_kv_heads, self.head_dim, 0))
+        ws = attention_workspace(q.device, ws_bytes)
         if context.block_tables is None:
             k = k.to(compute) if k.dtype != compute else k
             v = v.to(compute) if v.dtype != compute else v
@@ -273,10 +281,9 @@ class PagedAttention(nn.Module):
                 lib.nvs_varlen_attention(
                     q.data_ptr(), q.stride(0), q.stride(1),
                     k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1), v.stride(0), v.stride(1),
-                    cu_q.data_ptr(), cu_k.data_ptr(), B, T,
-                    int(context.max_seqlen_q), int(context.max_seqlen_k),
+                    cu_q.data_ptr(), cu_k.data_ptr(), B, T, max_q, max_k,
                     self.num_heads, self.num_kv_heads, self.head_dim, scale,
-                    out.data_ptr(), out.stride(0), out.stride(1), stream,
+                    out.data_ptr(), out.stride(0), out.stride(1), _lib.ptr(ws), ws_bytes, stream,
                 ),
                 "varlen_attention",
             )
@@ -296,10 +303,6 @@ class PagedAttention(nn.Module):
             if bt.dtype != torch.int32 or not bt.is_contiguous():
                 bt = bt.to(torch.int32).contiguous()
             num_blocks, block_size = kc.shape[0], kc.shape[1]
-            max_q, max_k = int(context.max_seqlen_q), int(context.max_seqlen_k)
-            ws_bytes = int(lib.nvs_attention_workspace_bytes(
-                B, max_q, max_k, self.num_heads, self.num_kv_heads, self.head_dim, block_size))
-            ws = attention_workspace(q.device, ws_bytes)
             _lib.check(
                 lib.nvs_paged_attention(
                     q.data_ptr(), q.stride(0), q.stride(1),

@@ -1,6 +1,8 @@
 """HIP attention vs the fp32 CPU oracle on the measured shapes and on edge
 cases.  Tolerances: bf16 KV max-abs <= 2e-2 and mean-abs <= 2e-3; int8 / fp8
-KV max-abs <= 5e-2 (tests/gpu_util.py).  Large batches are checked on a
+KV max-abs <= 5e-2; the max-abs bound applies on top of the half-ulp
+(2^-8 |ref|) that rounding the output to bf16 costs the reference itself
+(tests/gpu_util.py).  Large batches are checked on a
 subset of their sequences (the per-sequence math does not depend on the
 others) plus size-independent properties at full size."""
 import numpy as np
@@ -67,6 +69,9 @@ def test_decode_8b_subset_and_permutation(device):
         setattr(wl.attn, name, new)
     bt = wl.context.block_tables
     wl.context.block_tables = torch.where(bt >= 0, inv[bt.clamp(min=0).long()].int(), bt)
+    sl = wl.context.slot_mapping.long()
+    bs = wl.block_size
+    wl.context.slot_mapping = (inv[sl // bs] * bs + sl % bs).int()
     moved = wl.attn.forward(wl.q, wl.k, wl.v, wl.context)
     torch.cuda.synchronize()
     assert torch.equal(base, moved)

@@ -163,6 +163,9 @@ def test_c_abi_validates_before_launch():
     rc = lib.nvs_paged_attention(P, 1024, 128, P, P, 0, None, None, P, P, P, 32, 2, 2, 1, 4096,
                                  4, 1, 128, 256, 8, 0.125, P, 512, 128, None, 0, None)
     assert rc == -3 and b"workspace" in lib.nvs_last_error()
+    rc = lib.nvs_paged_attention(P, 1024, 128, P, P, 0, None, None, P, P, P, 32, 2, 2, 1, 4096,
+                                 4, 1, 128, 256, 8, 0.125, P, 512, 128, P + 16, 1 << 30, None)
+    assert rc == -3 and b"256-byte aligned" in lib.nvs_last_error()
     rc = lib.nvs_store_kvcache(P, P, 0, 1024, 128, 1024, 128, P, 4, P, P, 3, None, None, 8, 256,
                                8, 128, None)
     assert rc == -1 and b"k_scale" in lib.nvs_last_error()
@@ -173,7 +176,17 @@ def test_c_abi_validates_before_launch():
 
 
 def test_workspace_bytes():
+    """Plan (256-byte header + decode list + prefill list, each 256-aligned)
+    followed by the decode partials (only when there is more than one
+    256-key partition)."""
     lib = _lib.load()
-    assert lib.nvs_attention_workspace_bytes(64, 1, 256, 32, 8, 128, 256) == 0
+    a256 = lambda x: (x + 255) // 256 * 256
+    # 64 decode rows, max_k 256: one partition, plan only
+    assert lib.nvs_attention_workspace_bytes(64, 1, 256, 32, 8, 128, 256) == a256(256 + a256(64 * 4) + a256(64 * 4))
+    # max_k 8192: 32 partitions of partials
     n = lib.nvs_attention_workspace_bytes(64, 1, 8192, 32, 8, 128, 256)
-    assert n == 64 * 32 * 32 * 130 * 4
+    plan = a256(256 + a256(64 * 32 * 4) + a256(64 * 1 * 4))
+    assert n == plan + 64 * 32 * 32 * 130 * 4
+    # prefill tiles of 128 rows
+    n = lib.nvs_attention_workspace_bytes(16, 4096, 256, 32, 8, 128, 256)
+    assert n == a256(256 + a256(16 * 4) + a256(16 * 32 * 4))
