@@ -156,33 +156,73 @@ def bench_mixed(steps, warmup):
     return out
 
 
-def cpu_baseline(wl, decode_res):
-    """The eager restatement (gather + per-sequence fp32 attention) on the
-    host cores, over a bounded sample of the decode batch."""
-    import numpy as np
+def cpu_threads() -> int:
+    """Host threads for the CPU leg: the job's OpenMP share when set (the GPU
+    host's per-GPU share), else every visible core."""
+    try:
+        return max(1, int(os.environ["OMP_NUM_THREADS"]))
+    except (KeyError, ValueError):
+        return os.cpu_count() or 1
 
+
+def cpu_baseline(wl, budget_s: float = 10.0):
+    """The eager restatement (gather + per-sequence fp32 attention, the
+    reference's torch path) on the host cores, over a bounded sample of the
+    decode batch: whole passes over the batch's sequences, repeated until
+    about `budget_s` seconds of CPU work are done.  Unit: decode bytes / s,
+    the GPU figure's unit."""
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
-    from tests.gpu_util import oracle_paged
+    from oracle import attn_oracle
+    from tests.gpu_util import oracle_paged_inputs
 
-    torch.set_num_threads(os.cpu_count() or 1)
-    ids = list(range(4))
-    lens = [wl.seqs[i].num_cached_tokens + 1 for i in ids]
-    H, D = wl.num_kv_heads, wl.head_dim
-    nbytes = sum(lens) * H * 2 * D * 2 + len(ids) * wl.num_heads * D * 4
-    oracle_paged(wl, ids)  # warm-up
-    times = []
-    for _ in range(3):
+    torch.set_num_threads(cpu_threads())
+    H, D, Hq = wl.num_kv_heads, wl.head_dim, wl.num_heads
+    # Inputs are brought to host memory first (untimed): the CPU path, like
+    # the GPU one, starts from resident data.
+    inputs = [oracle_paged_inputs(wl, [i])[0] for i in range(wl.num_seqs)]
+    attn_oracle.paged_attention(*inputs[0])  # warm-up
+    nbytes, seqs, t = 0, 0, 0.0
+    while t < budget_s and seqs < 64 * wl.num_seqs:
+        i = seqs % wl.num_seqs
+        ctx = wl.seqs[i].num_cached_tokens + wl.seqs[i].num_new_tokens
         t0 = time.perf_counter()
-        oracle_paged(wl, ids)
-        times.append(time.perf_counter() - t0)
-    t = statistics.median(times)
+        attn_oracle.paged_attention(*inputs[i])
+        t += time.perf_counter() - t0
+        nbytes += ctx * H * 2 * D * 2 + Hq * D * 2 * 2
+        seqs += 1
+    del inputs
     return {
-        "value": nbytes / t / 1e9,
+        "value": round(nbytes / t / 1e9, 4),
         "unit": "GB/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": f"decode_8b sequences 0-3 ({sum(lens)} context tokens): gather + fp32 attention, median of 3",
+        "sample": f"decode_8b, {seqs} sequence decodes in batch order ({nbytes / 1e9:.2f} GB of K/V/q/o), "
+                  f"{t:.1f} s: per-sequence gather + fp32 attention from host memory",
     }
+
+
+def decode_traffic():
+    """HBM bytes per decode call as measured by the committed rocprofv3 PMC
+    runs (FETCH_SIZE + WRITE_SIZE, scaled by a plain copy's readings), or
+    None when no measurement is committed."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "decode_8b_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f)["bytes_per_call"]
+    except (OSError, ValueError, KeyError):
+        return None
+
+
+def calib_copy(nbytes: int = 1 << 30, reps: int = 5):
+    """A plain device copy of known size: reads and writes `nbytes` per
+    launch; its FETCH_SIZE / WRITE_SIZE readings scale the counters of the
+    attention kernels to bytes."""
+    src = torch.empty(nbytes // 2, dtype=torch.bfloat16, device="cuda").normal_()
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calib_copy_bytes": nbytes, "reps": reps}))
 
 
 def main():
@@ -192,6 +232,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--only", choices=["decode", "prefill", "quant", "mixed"], default=None)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="only run a 1 GiB device copy (for scaling PMC byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (the path has no multi-GPU code); got --gpus {args.gpus}",
@@ -205,6 +247,9 @@ def main():
     _lib.load()
     torch.cuda.set_device(0)
     steps, warmup = args.steps, args.warmup
+    if args.calib_copy:
+        calib_copy()
+        return
 
     if args.only == "prefill":
         print(json.dumps(bench_prefill(steps, warmup)))
@@ -244,14 +289,14 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(dec["gbs_attention"] / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": decode_traffic(),
         },
         "decode_8b": dec,
     }
     if args.only is None:
         if not args.no_cpu:
             log("cpu baseline")
-            line["cpu_baseline"] = cpu_baseline(wl, dec)
+            line["cpu_baseline"] = cpu_baseline(wl)
         del wl
         torch.cuda.empty_cache()
         line["prefill_8b"] = bench_prefill(max(5, steps // 4), 2)

@@ -79,41 +79,64 @@ __device__ __forceinline__ bf16x8 codes8_to_bf16x8(uint32_t lo, uint32_t hi) {
 // persistent grid and never dispatch empty work-groups (each costs the
 // dispatcher several nanoseconds; an upper-bound grid is mostly empty on
 // ragged batches).
-//   decode list:  b * max_parts + p, one entry per (q_len == 1 row, 256-key
-//                 partition); a row with no visible key gets one entry.
+//   decode records: one DecodeItem per (q_len == 1 row, 256-key partition),
+//                 self-contained (row, key range and the partition's block
+//                 ids), so a decode wave starts an item with one load that
+//                 it issued during the previous item instead of a chain of
+//                 dependent cu_seqlens / block-table loads; a row with no
+//                 visible key gets one record.
 //   prefill list: b * ntq + qt, one entry per (q_len > 1 row, 128-row query
 //                 tile), every row's tiles in descending qt (heaviest first).
 // ---------------------------------------------------------------------------
 constexpr int kPrefillBM = 128;  // query rows per prefill work item
 
+// Block ids a decode partition can span (block_size >= 64).
+constexpr int kDecodeItemBlocks = kDecodePart / 64;
+
+struct DecodeItem {
+  int q0;    // query / output row
+  int b;     // sequence (row of cu_seqlens)
+  int p;     // partition: keys [p * kDecodePart, kend)
+  int kend;  // min((p + 1) * kDecodePart, k_len); k_len (<= 0) for a row without keys
+  int blk[kDecodeItemBlocks];  // block ids of the partition's blocks in order,
+                               // -1 where the table has none or it is outside the pool
+};
+constexpr int kDecodeItemWords = (int)(sizeof(DecodeItem) / 4);
+static_assert(sizeof(DecodeItem) % 16 == 0, "decode records are read in 16-byte units");
+
 struct PlanHeader {
   int n_decode;
   int n_prefill;
-  int pad[62];  // keeps the lists 256-byte aligned
+  int prefill_next[8];  // per-XCD work counters of the prefill kernel (zeroed by the plan)
+  int pad[54];          // keeps the lists 256-byte aligned
 };
+static_assert(sizeof(PlanHeader) == 256, "plan header is one 256-byte line");
 
 struct Plan {
   PlanHeader* hdr;
-  int* dlist;
+  DecodeItem* drec;
   int* plist;
-  int max_parts;  // decode partitions per sequence (list stride)
+  int max_parts;  // decode partitions per sequence (bound of the record list)
   int ntq;        // prefill query tiles per sequence (list stride)
 };
 
 inline int64_t align256(int64_t x) { return (x + 255) & ~(int64_t)255; }
 
+inline int64_t decode_records_bytes(int B, int max_parts) {
+  return align256((int64_t)B * max_parts * (int64_t)sizeof(DecodeItem));
+}
+
 // Bytes of the plan for a batch; it sits at the start of the workspace.
 inline int64_t plan_bytes(int B, int max_parts, int ntq) {
-  return (int64_t)sizeof(PlanHeader) + align256((int64_t)B * max_parts * 4) +
-         align256((int64_t)B * ntq * 4);
+  return (int64_t)sizeof(PlanHeader) + decode_records_bytes(B, max_parts) + align256((int64_t)B * ntq * 4);
 }
 
 inline Plan plan_at(void* ws, int B, int max_parts, int ntq) {
   Plan p;
   char* c = (char*)ws;
   p.hdr = (PlanHeader*)c;
-  p.dlist = (int*)(c + sizeof(PlanHeader));
-  p.plist = (int*)(c + sizeof(PlanHeader) + align256((int64_t)B * max_parts * 4));
+  p.drec = (DecodeItem*)(c + sizeof(PlanHeader));
+  p.plist = (int*)(c + sizeof(PlanHeader) + decode_records_bytes(B, max_parts));
   p.max_parts = max_parts;
   p.ntq = ntq;
   return p;

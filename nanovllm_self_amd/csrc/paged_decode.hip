@@ -108,38 +108,40 @@ __device__ __forceinline__ LaneOffsets lane_offsets(int Hkv, int col, int grp) {
   return o;
 }
 
-// Block ids of the (at most kDecodePart / 64) blocks a partition spans,
-// looked up once when the wave starts, before any tile load is in flight: a
-// lookup between tile loads would have to wait for all of them.
-struct PartitionBlocks {
-  int lb0;       // logical block of the partition's first key
-  int id[kDecodePart / 64];
+// One decode work item as the wave holds it: scalars plus the block ids of
+// the partition in a vector value (a private array here would be placed in
+// LDS and re-read per tile).
+typedef int idxvec __attribute__((ext_vector_type(kDecodeItemBlocks)));
+
+struct ItemRegs {
+  int q0, b, p, kend;
+  int lb0;      // logical block of the partition's first key
+  idxvec blk;   // -1: missing block
 };
 
-__device__ __forceinline__ PartitionBlocks partition_blocks(const DecodeArgs& a, int b, int kbeg, int kend) {
-  PartitionBlocks pb;
-  pb.lb0 = kbeg / a.bs;
-  const int lb1 = (kend - 1) / a.bs;
+// Scalars of a record from its words.
+__device__ __forceinline__ ItemRegs unpack_item(const int (&w)[kDecodeItemWords], int bs) {
+  ItemRegs it;
+  it.q0 = w[0];
+  it.b = w[1];
+  it.p = w[2];
+  it.kend = w[3];
+  it.lb0 = it.p * kDecodePart / bs;
 #pragma unroll
-  for (int j = 0; j < kDecodePart / 64; ++j) {
-    const int lblk = pb.lb0 + j;
-    int blk = -1;
-    if (lblk <= lb1 && lblk < a.bt_stride) blk = a.bt[b * a.bt_stride + lblk];
-    pb.id[j] = __builtin_amdgcn_readfirstlane(blk);
-  }
-  return pb;
+  for (int j = 0; j < kDecodeItemBlocks; ++j) it.blk[j] = w[4 + j];
+  return it;
 }
 
 template <int KV>
 __device__ __forceinline__ void decode_load(DecodeTile<KV>& T, const DecodeArgs& a, const LaneOffsets& lo,
-                                            const PartitionBlocks& pb, int h, int kt) {
+                                            const ItemRegs& it, int h, int kt) {
   constexpr int ESZ = (KV == NVS_DTYPE_BF16) ? 2 : 1;
   const int lblk = kt / a.bs;
-  const int j = lblk - pb.lb0;
-  int blk = pb.id[0];
+  const int j = lblk - it.lb0;
+  int blk = it.blk[0];
 #pragma unroll
-  for (int i = 1; i < kDecodePart / 64; ++i) blk = (j == i) ? pb.id[i] : blk;
-  T.has = blk >= 0 && blk < a.NB;  // never read outside the pool
+  for (int i = 1; i < kDecodeItemBlocks; ++i) blk = (j == i) ? it.blk[i] : blk;
+  T.has = blk >= 0;  // the plan stores -1 for missing and out-of-pool blocks
   const int64_t row0 = ((int64_t)(T.has ? blk : 0) * a.bs + (kt - lblk * a.bs)) * a.Hkv + h;
   const char* kb = (const char*)a.kc + row0 * kHeadDim * ESZ;
   const char* vb = (const char*)a.vc + row0 * kHeadDim * ESZ;
@@ -324,14 +326,13 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-// One work item: (decode sequence b, kv head h, partition p).
+// One work item: (decode sequence, kv head h, partition), as planned.
 template <int KV, int NBUF>
-__device__ __forceinline__ void paged_decode_item(const DecodeArgs& a, int b, int h, int p) {
+__device__ __forceinline__ void paged_decode_item(const DecodeArgs& a, const ItemRegs& it, int h) {
   const int lane = threadIdx.x;
-  const int q0 = a.cu_q[b];
-  const int klen = a.cu_k[b + 1] - a.cu_k[b];
+  const int q0 = it.q0, b = it.b, p = it.p;
   const int kbeg = p * kDecodePart;
-  if (kbeg >= klen) {
+  if (kbeg >= it.kend) {
     if (p == 0 && a.max_parts == 1) {  // no visible key: output 0 (the merge handles max_parts > 1)
       for (int i = lane; i < a.g * (kHeadDim / 2); i += 64) {
         const int c = i / (kHeadDim / 2), d = 2 * (i % (kHeadDim / 2));
@@ -340,7 +341,7 @@ __device__ __forceinline__ void paged_decode_item(const DecodeArgs& a, int b, in
     }
     return;
   }
-  const int kend = min(kbeg + kDecodePart, klen);
+  const int kend = it.kend;
   const int ntiles = (kend - kbeg + 31) >> 5;
   const int col = lane & 15, grp = lane >> 4;
 
@@ -374,18 +375,17 @@ __device__ __forceinline__ void paged_decode_item(const DecodeArgs& a, int b, in
   // order and each wait covers exactly the tile about to be used.
   constexpr int NT = kDecodePart / 32;
   const LaneOffsets lo = lane_offsets<KV>(a.Hkv, col, grp);
-  const PartitionBlocks pb = partition_blocks(a, b, kbeg, kend);
   DecodeTile<KV> ring[NBUF];
   const int last = ntiles - 1;
 #pragma unroll
   for (int i = 0; i < NBUF - 1; ++i) {
-    decode_load<KV>(ring[i], a, lo, pb, h, kbeg + 32 * min(i, last));
+    decode_load<KV>(ring[i], a, lo, it, h, kbeg + 32 * min(i, last));
     __builtin_amdgcn_sched_barrier(0);
   }
 #pragma unroll
   for (int i = 0; i < NT; ++i) {
     if (i + NBUF - 1 < NT)
-      decode_load<KV>(ring[(i + NBUF - 1) % NBUF], a, lo, pb, h, kbeg + 32 * min(i + NBUF - 1, last));
+      decode_load<KV>(ring[(i + NBUF - 1) % NBUF], a, lo, it, h, kbeg + 32 * min(i + NBUF - 1, last));
     __builtin_amdgcn_sched_barrier(0);
     if (i < last) {  // every tile but the last is full: no masking
       if (!ring[i % NBUF].has) zero_tile(ring[i % NBUF]);
@@ -440,18 +440,30 @@ __device__ __forceinline__ void paged_decode_item(const DecodeArgs& a, int b, in
   }
 }
 
-// Persistent: each wave walks the plan's decode list with a grid stride, kv
-// head fastest, so the Hkv waves reading one block's rows run side by side.
+// Persistent: each wave walks the plan's decode records with a grid stride,
+// kv head fastest, so the Hkv waves reading one block's rows run side by
+// side.  The next item's record is loaded while the current item runs: it
+// comes through the scalar cache (the restrict-qualified pointer lets the
+// compiler prove no store of this kernel clobbers it), so waiting for it never
+// waits for this wave's vector loads or stores.
 template <int KV>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kDecodeWavesPerEU)))
-void paged_decode_kernel(DecodeArgs a) {
+void paged_decode_kernel(DecodeArgs a, const int* __restrict__ rec_words) {
   const int total = a.plan.hdr->n_decode * a.Hkv;
-  for (int k = blockIdx.x; k < total; k += gridDim.x) {
-    const int idx = k / a.Hkv;
-    const int h = k - idx * a.Hkv;
-    const int item = __builtin_amdgcn_readfirstlane(a.plan.dlist[idx]);
-    const int b = item / a.max_parts;
-    paged_decode_item<KV, kDecodeBuffers>(a, b, h, item - b * a.max_parts);
+  int k = blockIdx.x;
+  if (k >= total) return;
+  int w[kDecodeItemWords];
+  const int* r = rec_words + (int64_t)(k / a.Hkv) * kDecodeItemWords;
+#pragma unroll
+  for (int i = 0; i < kDecodeItemWords; ++i) w[i] = r[i];
+  for (; k < total; k += gridDim.x) {
+    const int h = k % a.Hkv;
+    const ItemRegs it = unpack_item(w, a.bs);
+    const int kn = min(k + (int)gridDim.x, total - 1);
+    r = rec_words + (int64_t)(kn / a.Hkv) * kDecodeItemWords;
+#pragma unroll
+    for (int i = 0; i < kDecodeItemWords; ++i) w[i] = r[i];
+    paged_decode_item<KV, kDecodeBuffers>(a, it, h);
   }
 }
 
@@ -528,15 +540,16 @@ int launch_decode(const AttnParams& P, const Plan& plan, void* partials, hipStre
   const int64_t upper = (int64_t)P.B * a.max_parts * P.Hkv;
   const int waves = (int)std::min<int64_t>(upper, device_slots(4 * kDecodeWavesPerEU));
   dim3 grid(waves), block(64);
+  const int* words = reinterpret_cast<const int*>(plan.drec);
   switch (P.cache_dtype) {
     case NVS_DTYPE_BF16:
-      hipLaunchKernelGGL(paged_decode_kernel<NVS_DTYPE_BF16>, grid, block, 0, stream, a);
+      hipLaunchKernelGGL(paged_decode_kernel<NVS_DTYPE_BF16>, grid, block, 0, stream, a, words);
       break;
     case NVS_DTYPE_INT8:
-      hipLaunchKernelGGL(paged_decode_kernel<NVS_DTYPE_INT8>, grid, block, 0, stream, a);
+      hipLaunchKernelGGL(paged_decode_kernel<NVS_DTYPE_INT8>, grid, block, 0, stream, a, words);
       break;
     case NVS_DTYPE_FP8_E4M3:
-      hipLaunchKernelGGL(paged_decode_kernel<NVS_DTYPE_FP8_E4M3>, grid, block, 0, stream, a);
+      hipLaunchKernelGGL(paged_decode_kernel<NVS_DTYPE_FP8_E4M3>, grid, block, 0, stream, a, words);
       break;
     default:
       set_error("paged_attention: decode does not serve cache dtype %d", P.cache_dtype);

@@ -343,26 +343,42 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int b, int qt
   }
 }
 
-// Persistent: each work-group walks the plan's prefill list.  Work k maps to
-// (unit u, head-in-group c) with u = (list index, kv head) and k % 8 == u % 8,
-// so with a grid that is a multiple of 8 the g query heads of a unit run on
-// one XCD and fetch its K/V tiles into that XCD's L2 once.
+// Persistent, dynamically scheduled: work k maps to (unit u, head-in-group
+// c) with u = (list index, kv head); work with k % 8 == x is claimed from XCD
+// x's counter by the work-groups on XCD x (work-group i runs on XCD i % 8), so
+// the g query heads of a unit run on one XCD and fetch its K/V tiles into that
+// XCD's L2 once, and each XCD's work-groups take the heaviest remaining work
+// first.  The next claim is made while the current item runs.
 template <int KV, bool PAGED>
 __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t Ks[kBN * kKStride];
   __shared__ __attribute__((aligned(16))) uint16_t Vt[kHeadDim * kVStride];
+  __shared__ int s_claim[2];
   const int units = a.plan.hdr->n_prefill * a.Hkv;
   const int total = ((units + 7) / 8) * 8 * a.g;
-  for (int k = blockIdx.x; k < total; k += gridDim.x) {
-    const int xcd = k & 7, r8 = k >> 3;
-    const int cg = r8 % a.g;
-    const int u = 8 * (r8 / a.g) + xcd;
-    if (u >= units) continue;
-    const int idx = u / a.Hkv;
-    const int hkv = u - idx * a.Hkv;
-    const int item = __builtin_amdgcn_readfirstlane(a.plan.plist[idx]);
-    const int b = item / a.plan.ntq;
-    prefill_item<KV, PAGED>(a, b, item - b * a.plan.ntq, hkv, cg, Ks, Vt);
+  const int xcd = blockIdx.x & 7;
+  int* counter = a.plan.hdr->prefill_next + xcd;
+  if (threadIdx.x == 0) s_claim[0] = atomicAdd(counter, 1);
+  __syncthreads();
+  for (int it = 0;; ++it) {
+    const int c = s_claim[it & 1];
+    const int k = 8 * c + xcd;
+    if (k >= total) break;
+    int next = 0;
+    if (threadIdx.x == 0) next = atomicAdd(counter, 1);
+    const int cg = c % a.g;
+    const int u = 8 * (c / a.g) + xcd;
+    if (u < units) {
+      const int idx = u / a.Hkv;
+      const int hkv = u - idx * a.Hkv;
+      const int item = __builtin_amdgcn_readfirstlane(a.plan.plist[idx]);
+      const int b = item / a.plan.ntq;
+      prefill_item<KV, PAGED>(a, b, item - b * a.plan.ntq, hkv, cg, Ks, Vt);
+    }
+    // The claim slot read next iteration was last read two iterations ago,
+    // before the barrier below.
+    if (threadIdx.x == 0) s_claim[(it + 1) & 1] = next;
+    __syncthreads();
   }
 }
 

@@ -46,10 +46,11 @@ def cache_blocks_f32(attn, blocks: np.ndarray):
     return out[0], out[1]
 
 
-def oracle_paged(wl, seq_ids):
-    """fp32 oracle output rows of the given sequences of a paged workload.
-    Only their blocks are copied from the device; block ids are remapped onto
-    that compact pool."""
+def oracle_paged_inputs(wl, seq_ids):
+    """Host-side oracle inputs for the given sequences of a paged workload:
+    only their blocks are copied from the device, block ids remapped onto that
+    compact pool.  Returns (positional args of attn_oracle.paged_attention,
+    the sequences' query rows)."""
     ctx = wl.context
     cu_q = ctx.cu_seqlens_q.cpu().tolist()
     bs = wl.block_size
@@ -72,9 +73,14 @@ def oracle_paged(wl, seq_ids):
     q = torch.from_numpy(bf16_to_np(wl.q[torch.as_tensor(qrows, device=wl.q.device)]))
     sub_cu_q = np.concatenate([[0], np.cumsum(qlens)]).tolist()
     sub_cu_k = np.concatenate([[0], np.cumsum(lens)]).tolist()
-    out = AO.paged_attention(q, kv, vv, bt, sub_cu_q, sub_cu_k, lens, wl.num_heads, wl.num_kv_heads,
-                             wl.head_dim)
-    return out.numpy(), qrows
+    args = (q, kv, vv, bt, sub_cu_q, sub_cu_k, lens, wl.num_heads, wl.num_kv_heads, wl.head_dim)
+    return args, qrows
+
+
+def oracle_paged(wl, seq_ids):
+    """fp32 oracle output rows of the given sequences of a paged workload."""
+    args, qrows = oracle_paged_inputs(wl, seq_ids)
+    return AO.paged_attention(*args).numpy(), qrows
 
 
 def compare(got: np.ndarray, ref: np.ndarray, quant: bool, what: str):

@@ -243,6 +243,44 @@ def test_mixed_32b_decode_rows(device):
     _check(wl, ids, "mixed_32b decode rows")
 
 
+@pytest.mark.parametrize("bs", [64, 128])
+@pytest.mark.parametrize("kv", ["bf16", "fp8"])
+def test_small_blocks(device, bs, kv):
+    """block_size below the 256-key decode partition: one partition spans
+    several blocks (decode), and prefill key tiles cross block boundaries."""
+    say(f"block_size {bs} {kv}")
+    dec = [700, 1000, 1537, 63, 256]
+    pre = [(bs * 3, 200), (0, 333)]
+    lens = dec + [p + n for p, n in pre]
+    NB = sum((n + bs - 1) // bs for n in lens) + 3
+    tabs = _tables(lens, NB, 30 + bs, bs=bs)
+    seqs = [SeqSlice(tabs[i], n - 1, 1) for i, n in enumerate(dec)]
+    seqs += [SeqSlice(tabs[len(dec) + j], p, n) for j, (p, n) in enumerate(pre)]
+    wl = _custom(seqs, 8, 2, NB, kv=kv, seed=31 + bs, bs=bs)
+    _check(wl, what=f"block_size {bs}/{kv}")
+
+
+def test_more_rows_than_one_plan_chunk(device):
+    """More than 1024 rows: decode records are planned in chunks of rows and
+    prefill tiles take the general (level by level) ordering."""
+    say("1100-row batch")
+    g = torch.Generator().manual_seed(40)
+    n_dec, n_pre = 1080, 20
+    dec = torch.randint(1, 700, (n_dec,), generator=g).tolist()
+    pre = [(int(p), int(n)) for p, n in zip(torch.randint(0, 4, (n_pre,), generator=g).tolist(),
+                                            torch.randint(2, 300, (n_pre,), generator=g).tolist())]
+    pre = [(64 * p, n) for p, n in pre]
+    lens = dec + [p + n for p, n in pre]
+    bs = 64
+    NB = sum((n + bs - 1) // bs for n in lens)
+    tabs = _tables(lens, NB, 41, bs=bs)
+    seqs = [SeqSlice(tabs[i], n - 1, 1) for i, n in enumerate(dec)]
+    seqs += [SeqSlice(tabs[n_dec + j], p, n) for j, (p, n) in enumerate(pre)]
+    wl = _custom(seqs, 4, 2, NB, seed=42, bs=bs)
+    ids = list(range(0, n_dec, 37)) + [n_dec - 1] + list(range(n_dec, n_dec + n_pre))
+    _check(wl, ids, "1100-row batch")
+
+
 # ---------------------------------------------------------------- API
 def test_forward_profile_and_decode_entry(device):
     say("profile + decode_flashattn")

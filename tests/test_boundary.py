@@ -176,17 +176,17 @@ def test_c_abi_validates_before_launch():
 
 
 def test_workspace_bytes():
-    """Plan (256-byte header + decode list + prefill list, each 256-aligned)
-    followed by the decode partials (only when there is more than one
-    256-key partition)."""
+    """Plan (256-byte header + 32-byte decode records + prefill list, each
+    256-aligned) followed by the decode partials (only when there is more
+    than one 256-key partition)."""
     lib = _lib.load()
     a256 = lambda x: (x + 255) // 256 * 256
     # 64 decode rows, max_k 256: one partition, plan only
-    assert lib.nvs_attention_workspace_bytes(64, 1, 256, 32, 8, 128, 256) == a256(256 + a256(64 * 4) + a256(64 * 4))
+    assert lib.nvs_attention_workspace_bytes(64, 1, 256, 32, 8, 128, 256) == a256(256 + a256(64 * 32) + a256(64 * 4))
     # max_k 8192: 32 partitions of partials
     n = lib.nvs_attention_workspace_bytes(64, 1, 8192, 32, 8, 128, 256)
-    plan = a256(256 + a256(64 * 32 * 4) + a256(64 * 1 * 4))
+    plan = a256(256 + a256(64 * 32 * 32) + a256(64 * 1 * 4))
     assert n == plan + 64 * 32 * 32 * 130 * 4
     # prefill tiles of 128 rows
     n = lib.nvs_attention_workspace_bytes(16, 4096, 256, 32, 8, 128, 256)
-    assert n == a256(256 + a256(16 * 4) + a256(16 * 32 * 4))
+    assert n == a256(256 + a256(16 * 32) + a256(16 * 32 * 4))
