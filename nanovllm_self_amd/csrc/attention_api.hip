@@ -24,30 +24,42 @@ static int validate_common(const AttnParams& P, const char* who) {
 }
 
 namespace nvs {
-static int prefill_tiles(int max_seqlen_q) {
-  const int t = (max_seqlen_q + kPrefillBM - 1) / kPrefillBM;
+// Query positions per prefill tile for num_heads / num_kv_heads (the
+// smallest tile when the group size is unknown).
+static int prefill_pbm(int num_heads, int num_kv_heads) {
+  const int g = (num_kv_heads > 0 && num_heads % num_kv_heads == 0) ? num_heads / num_kv_heads : 0;
+  return prefill_positions(g);
+}
+
+static int prefill_tiles(int max_seqlen_q, int pbm) {
+  const int t = (max_seqlen_q + pbm - 1) / pbm;
   return t < 1 ? 1 : t;
 }
 
-int64_t attention_workspace_bytes(int num_seqs, int max_seqlen_q, int max_seqlen_k, int num_heads) {
+int64_t attention_workspace_bytes(int num_seqs, int max_seqlen_q, int max_seqlen_k, int num_heads,
+                                  int num_kv_heads) {
   if (num_seqs <= 0 || num_heads <= 0) return 0;
   const int parts = decode_max_parts(max_seqlen_k);
-  return align256(plan_bytes(num_seqs, parts, prefill_tiles(max_seqlen_q))) +
-         decode_workspace_bytes(num_seqs, max_seqlen_k, num_heads);
+  const int ntq = prefill_tiles(max_seqlen_q, prefill_pbm(num_heads, num_kv_heads));
+  return align256(plan_bytes(num_seqs, parts, ntq)) + decode_workspace_bytes(num_seqs, max_seqlen_k, num_heads);
+}
+
+static Plan make_plan(void* ws, const AttnParams& P) {
+  const int pbm = prefill_pbm(P.Hq, P.Hkv);
+  return plan_at(ws, P.B, decode_max_parts(P.max_seqlen_k), prefill_tiles(P.max_seqlen_q, pbm), pbm);
 }
 }  // namespace nvs
 
 extern "C" int64_t nvs_attention_workspace_bytes(int num_seqs, int max_seqlen_q, int max_seqlen_k,
                                                  int num_heads, int num_kv_heads, int head_dim,
                                                  int block_size) {
-  (void)num_kv_heads;
   (void)head_dim;
   (void)block_size;
-  return attention_workspace_bytes(num_seqs, max_seqlen_q, max_seqlen_k, num_heads);
+  return attention_workspace_bytes(num_seqs, max_seqlen_q, max_seqlen_k, num_heads, num_kv_heads);
 }
 
 static int check_workspace(const AttnParams& P, const char* who) {
-  const int64_t need = attention_workspace_bytes(P.B, P.max_seqlen_q, P.max_seqlen_k, P.Hq);
+  const int64_t need = attention_workspace_bytes(P.B, P.max_seqlen_q, P.max_seqlen_k, P.Hq, P.Hkv);
   NVS_REQUIRE(P.ws && P.ws_bytes >= need && ((uintptr_t)P.ws % 256) == 0, NVS_ERR_WORKSPACE,
               "%s: workspace of %lld bytes (256-byte aligned) needed, %lld given", who,
               (long long)need, (long long)P.ws_bytes);
@@ -101,7 +113,7 @@ extern "C" int nvs_paged_attention(const void* q, int64_t q_tok_stride, int64_t 
   rc = check_workspace(P, "paged_attention");
   if (rc != NVS_OK) return rc;
   hipStream_t s = (hipStream_t)stream;
-  const Plan plan = plan_at(workspace, num_seqs, decode_max_parts(max_seqlen_k), prefill_tiles(max_seqlen_q));
+  const Plan plan = make_plan(workspace, P);
   char* partials = (char*)workspace + align256(plan_bytes(num_seqs, plan.max_parts, plan.ntq));
   rc = launch_plan(P, plan, /*paged=*/true, s);
   if (rc != NVS_OK) return rc;
@@ -143,7 +155,7 @@ extern "C" int nvs_varlen_attention(const void* q, int64_t q_tok_stride, int64_t
   rc = check_workspace(P, "varlen_attention");
   if (rc != NVS_OK) return rc;
   hipStream_t s = (hipStream_t)stream;
-  const Plan plan = plan_at(workspace, num_seqs, decode_max_parts(max_seqlen_k), prefill_tiles(max_seqlen_q));
+  const Plan plan = make_plan(workspace, P);
   rc = launch_plan(P, plan, /*paged=*/false, s);
   if (rc != NVS_OK) return rc;
   return launch_prefill(P, plan, s);

@@ -85,10 +85,21 @@ __device__ __forceinline__ bf16x8 codes8_to_bf16x8(uint32_t lo, uint32_t hi) {
 //                 it issued during the previous item instead of a chain of
 //                 dependent cu_seqlens / block-table loads; a row with no
 //                 visible key gets one record.
-//   prefill list: b * ntq + qt, one entry per (q_len > 1 row, 128-row query
-//                 tile), every row's tiles in descending qt (heaviest first).
+//   prefill list: b * ntq + qt, one entry per (q_len > 1 row, tile of
+//                 prefill_positions(g) query positions), every row's tiles in
+//                 descending qt (heaviest first).
 // ---------------------------------------------------------------------------
-constexpr int kPrefillBM = 128;  // query rows per prefill work item
+
+// Prefill work item: one 8-wave work-group serves up to 8 query heads of one
+// kv head (all of them when g <= 8) over a tile of query positions, 32 rows
+// (positions) per wave; fewer heads per item means more positions per item.
+constexpr int kPrefillWaves = 8;
+constexpr int kPrefillWaveRows = 32;
+__host__ __device__ inline int prefill_heads_per_item(int g) { return g < kPrefillWaves ? g : kPrefillWaves; }
+__host__ __device__ inline int prefill_positions(int g) {
+  return g <= 0 ? kPrefillWaveRows : kPrefillWaveRows * (kPrefillWaves / prefill_heads_per_item(g));
+}
+__host__ __device__ inline int prefill_head_groups(int g) { return (g + kPrefillWaves - 1) / kPrefillWaves; }
 
 // Block ids a decode partition can span (block_size >= 64).
 constexpr int kDecodeItemBlocks = kDecodePart / 64;
@@ -118,6 +129,7 @@ struct Plan {
   int* plist;
   int max_parts;  // decode partitions per sequence (bound of the record list)
   int ntq;        // prefill query tiles per sequence (list stride)
+  int pbm;        // query positions per prefill tile
 };
 
 inline int64_t align256(int64_t x) { return (x + 255) & ~(int64_t)255; }
@@ -131,7 +143,7 @@ inline int64_t plan_bytes(int B, int max_parts, int ntq) {
   return (int64_t)sizeof(PlanHeader) + decode_records_bytes(B, max_parts) + align256((int64_t)B * ntq * 4);
 }
 
-inline Plan plan_at(void* ws, int B, int max_parts, int ntq) {
+inline Plan plan_at(void* ws, int B, int max_parts, int ntq, int pbm) {
   Plan p;
   char* c = (char*)ws;
   p.hdr = (PlanHeader*)c;
@@ -139,6 +151,7 @@ inline Plan plan_at(void* ws, int B, int max_parts, int ntq) {
   p.plist = (int*)(c + sizeof(PlanHeader) + decode_records_bytes(B, max_parts));
   p.max_parts = max_parts;
   p.ntq = ntq;
+  p.pbm = pbm;
   return p;
 }
 
@@ -179,7 +192,8 @@ struct AttnParams {
 };
 
 int64_t decode_workspace_bytes(int num_seqs, int max_seqlen_k, int num_heads);
-int64_t attention_workspace_bytes(int num_seqs, int max_seqlen_q, int max_seqlen_k, int num_heads);
+int64_t attention_workspace_bytes(int num_seqs, int max_seqlen_q, int max_seqlen_k, int num_heads,
+                                  int num_kv_heads);
 int launch_plan(const AttnParams& P, const Plan& plan, bool paged, hipStream_t stream);
 int launch_decode(const AttnParams& P, const Plan& plan, void* partials, hipStream_t stream);
 int launch_prefill(const AttnParams& P, const Plan& plan, hipStream_t stream);

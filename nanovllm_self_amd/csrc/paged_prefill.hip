@@ -10,18 +10,26 @@
 // dequantize_int8_per_token rounding (:100-117).  Local mode reads the step's
 // k/v rows directly (block_tables is None).
 //
-// Work decomposition: one 256-thread work-group per (sequence, 128-row query
-// tile, query head).  Each wave owns 32 query rows.  Per 64-key tile, K
-// (row-major) and V^T are staged in LDS by all four waves; then each wave
-//   S^T[64 x 32] = K . Q^T         (32 x mfma_f32_16x16x32_bf16)
-//   O^T[128 x 32] += V^T . P^T     (32 x mfma_f32_16x16x32_bf16)
-// P^T is consumed from registers: the S^T accumulator layout equals the
-// B-operand layout of the PV product.  The next tile's global loads are in
-// flight while the current tile is computed.
+// Work decomposition: one 512-thread work-group (8 waves, two per SIMD) per
+// (sequence, tile of query positions, kv head, group of up to 8 query heads).
+// Each wave owns 32 query positions of one query head, so the g heads that
+// share a kv head share every K/V tile the work-group stages.  Per 64-key
+// tile, K and V are staged row-major in LDS (double-buffered: the next tile's
+// global loads are in flight during the current tile, one barrier per tile)
+// and each wave computes, with v_mfma_f32_32x32x16_bf16,
+//   S^T[64 keys x 32 q] = K . Q^T      (16 MFMAs; Q^T stays in registers)
+//   O^T[128 d x 32 q] += V^T . P^T     (16 MFMAs)
+// The S^T accumulator layout (lane = query column, keys along registers) is
+// the B-operand layout of P^T, so P never leaves registers; the V^T operand
+// is read from the row-major V tile with ds_read_b64_tr_b16, which transposes
+// 4 x 16 bf16 blocks across each 16-lane group.  One query per lane makes the
+// row max a single cross-lane exchange.  Two waves per SIMD let one wave's
+// softmax run under the other's MFMAs.
 //
-// Scheduling: work-groups are dispatched longest-first (last query tiles of
-// every sequence first) and the g query heads that share a kv head land on
-// the same XCD so their K/V tiles are fetched into that XCD's L2 once.
+// LDS tiles are row-major with 16-byte chunks XOR-swizzled per key
+// (chunk ^ swz(key)): both the K reads (16 keys x one chunk per 16 lanes)
+// and the transposed V reads (4 keys x 4 chunks per 16 lanes) hit 16
+// distinct 16-byte bank groups.
 #include <algorithm>
 
 #include "nvs_common.h"
@@ -29,10 +37,16 @@
 
 namespace nvs {
 
-constexpr int kBM = kPrefillBM;  // query rows per work item
-constexpr int kBN = 64;        // keys per tile
-constexpr int kKStride = 136;  // bf16 per K row in LDS (272 B: conflict-free b128 reads)
-constexpr int kVStride = 68;   // bf16 per V^T row in LDS (136 B: conflict-free b64 access)
+constexpr int kWaves = kPrefillWaves;  // 8
+constexpr int kThreads = 64 * kWaves;
+constexpr int kRows = kPrefillWaveRows;  // query positions per wave
+constexpr int kBN = 64;                  // keys per tile
+constexpr int kTile = kBN * kHeadDim;    // bf16 elements of one K (or V) tile
+constexpr int kBlockWindow = 512;        // block-table entries staged in LDS at a time
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x8 __attribute__((ext_vector_type(8)));
 
 struct PrefillArgs {
   const uint16_t* q;
@@ -42,9 +56,9 @@ struct PrefillArgs {
   const float* ks;
   const float* vs;
   const int32_t* bt;
-  int bt_stride;      // row stride == number of columns (32-bit: scalar lookup)
+  int bt_stride;  // row stride == number of columns
   int NB;
-  int64_t T;          // rows of the local k/v
+  int64_t T;  // rows of the local k/v
   int bs;
   const uint16_t* k;
   const uint16_t* v;
@@ -52,329 +66,353 @@ struct PrefillArgs {
   const int32_t* cu_q;
   const int32_t* cu_k;
   int B, Hq, Hkv, g;
+  int hpw, nblk, hgroups;  // heads per item, position blocks per item, head groups per kv head
   Plan plan;
   float scale_log2;
   uint16_t* out;
   int64_t out_ts, out_hs;
 };
 
-// Global-load staging of one K/V tile.
+// 16-byte chunk swizzle of key row `key`: a bijection of key % 16 that maps
+// 4 consecutive keys to 4 different chunk quads.
+__device__ __forceinline__ int swz(int key) { return ((key & 3) << 2) | ((key >> 2) & 3); }
+// Element offset of (key, d) in a swizzled tile (d a multiple of 4).
+__device__ __forceinline__ int tile_at(int key, int d) {
+  return key * kHeadDim + (((d >> 3) ^ swz(key)) << 3) + (d & 7);
+}
+
+// ---------------------------------------------------------------------------
+// Tile fill: global -> registers (issued a tile ahead) -> swizzled LDS.
+// bf16: thread t owns chunk t % 16 of key rows t / 16 and t / 16 + 32 of K
+// and V.  Codes: thread t owns 16 codes (d = 16 (t % 8) ..) of key row t / 8.
+// Rows past the sequence or in a missing block are zero.
+// ---------------------------------------------------------------------------
 template <int KV>
-struct FillRegs {
-  u32x4 k[4];  // K: key tid/16 + 16 i, d chunk tid%16 (8 elements)
-  u32x4 v[4];  // V: key 4 kg + e, d chunk 4 w + lane/16
+struct Fill {
+  u32x4 k[2], v[2];
+  bool ok[2];  // row holds a visible key (else stored as zeros)
 };
 template <>
-struct FillRegs<NVS_DTYPE_INT8> {
-  u32x2 k[4];
-  u32x2 v[4];
-  float ksc[4], vsc[4];
+struct Fill<NVS_DTYPE_INT8> {
+  u32x4 k, v;
+  float ks, vs;
+  bool ok;
 };
 template <>
-struct FillRegs<NVS_DTYPE_FP8_E4M3> {
-  u32x2 k[4];
-  u32x2 v[4];
-  float ksc[4], vsc[4];
+struct Fill<NVS_DTYPE_FP8_E4M3> {
+  u32x4 k, v;
+  float ks, vs;
+  bool ok;
 };
 
+struct ItemKV {
+  int b, hkv, k0, K;
+  int win0;  // first logical block staged in blk_lds
+};
+
+// Loads are issued unconditionally from in-bounds addresses (a missing block
+// reads block 0, a row outside the local k/v reads its first or last row) and replaced by
+// zeros when stored: with no load behind a branch and no use of the loaded
+// values before the store, the compiler's wait counts stay exact and the
+// compute never waits for the next tile's loads.
 template <int KV, bool PAGED>
-__device__ __forceinline__ void prefill_fill_load(FillRegs<KV>& R, const PrefillArgs& a, int b,
-                                                  int hkv, int k0, int K, int kt, int tid) {
-  const int lane = tid & 63, w = tid >> 6;
+__device__ __forceinline__ void fill_load(Fill<KV>& F, const PrefillArgs& a, const ItemKV& it, int kt,
+                                          const int* blk_lds) {
+  const int tid = threadIdx.x;
   int64_t slot0 = 0;
   bool have = true;
   if constexpr (PAGED) {
-    const int lblk = kt / a.bs;
-    const int blk = lblk < a.bt_stride ? a.bt[b * a.bt_stride + lblk] : -1;
-    have = blk >= 0 && blk < a.NB;  // never read outside the pool
-    slot0 = (int64_t)blk * a.bs + (kt - lblk * a.bs);
+    const int lblk = kt / a.bs;  // a 64-key tile never spans two blocks (bs % 64 == 0)
+    const int blk = blk_lds[lblk - it.win0];
+    have = blk >= 0;
+    slot0 = (int64_t)(have ? blk : 0) * a.bs + (kt - lblk * a.bs);
   }
-  // K rows
-  const int kc = tid & 15;
+  if constexpr (KV == NVS_DTYPE_BF16) {
+    const int c = tid & 15;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int key = (tid >> 4) + 16 * i;
-    const bool ok = have && (kt + key < K);
-    if constexpr (PAGED) {
-      const int64_t row = (slot0 + key) * a.Hkv + hkv;
-      if constexpr (KV == NVS_DTYPE_BF16) {
-        R.k[i] = ok ? *reinterpret_cast<const u32x4*>((const uint16_t*)a.kc + row * kHeadDim + 8 * kc)
-                    : u32x4{0, 0, 0, 0};
+    for (int i = 0; i < 2; ++i) {
+      const int key = (tid >> 4) + 32 * i;
+      F.ok[i] = have && kt + key < it.K;
+      if constexpr (PAGED) {
+        const int64_t row = (slot0 + key) * a.Hkv + it.hkv;
+        F.k[i] = *reinterpret_cast<const u32x4*>((const uint16_t*)a.kc + row * kHeadDim + 8 * c);
+        F.v[i] = *reinterpret_cast<const u32x4*>((const uint16_t*)a.vc + row * kHeadDim + 8 * c);
       } else {
-        R.k[i] = ok ? *reinterpret_cast<const u32x2*>((const uint8_t*)a.kc + row * kHeadDim + 8 * kc)
-                    : u32x2{0, 0};
-        R.ksc[i] = ok ? a.ks[row] : 0.0f;
+        const int64_t row = max((int64_t)0, min((int64_t)it.k0 + kt + key, a.T - 1));
+        F.k[i] = *reinterpret_cast<const u32x4*>(a.k + row * a.k_ts + (int64_t)it.hkv * a.k_hs + 8 * c);
+        F.v[i] = *reinterpret_cast<const u32x4*>(a.v + row * a.v_ts + (int64_t)it.hkv * a.v_hs + 8 * c);
       }
-    } else {
-      const bool in = ok && (int64_t)k0 + kt + key < a.T;
-      R.k[i] = in ? *reinterpret_cast<const u32x4*>(a.k + (int64_t)(k0 + kt + key) * a.k_ts +
-                                                    (int64_t)hkv * a.k_hs + 8 * kc)
-                  : u32x4{0, 0, 0, 0};
     }
-  }
-  // V rows
-  const int kg = lane & 15, vc = 4 * w + (lane >> 4);
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int key = 4 * kg + e;
-    const bool ok = have && (kt + key < K);
-    if constexpr (PAGED) {
-      const int64_t row = (slot0 + key) * a.Hkv + hkv;
-      if constexpr (KV == NVS_DTYPE_BF16) {
-        R.v[e] = ok ? *reinterpret_cast<const u32x4*>((const uint16_t*)a.vc + row * kHeadDim + 8 * vc)
-                    : u32x4{0, 0, 0, 0};
-      } else {
-        R.v[e] = ok ? *reinterpret_cast<const u32x2*>((const uint8_t*)a.vc + row * kHeadDim + 8 * vc)
-                    : u32x2{0, 0};
-        R.vsc[e] = ok ? a.vs[row] : 0.0f;
-      }
-    } else {
-      const bool in = ok && (int64_t)k0 + kt + key < a.T;
-      R.v[e] = in ? *reinterpret_cast<const u32x4*>(a.v + (int64_t)(k0 + kt + key) * a.v_ts +
-                                                    (int64_t)hkv * a.v_hs + 8 * vc)
-                  : u32x4{0, 0, 0, 0};
-    }
+  } else {
+    const int key = tid >> 3, c = tid & 7;
+    F.ok = have && kt + key < it.K;
+    const int64_t row = (slot0 + key) * a.Hkv + it.hkv;
+    F.k = *reinterpret_cast<const u32x4*>((const uint8_t*)a.kc + row * kHeadDim + 16 * c);
+    F.v = *reinterpret_cast<const u32x4*>((const uint8_t*)a.vc + row * kHeadDim + 16 * c);
+    F.ks = a.ks[row];
+    F.vs = a.vs[row];
   }
 }
 
 // 8 codes * scale -> 8 bf16 (RNE), as bf16(code.float() * scale).
 template <int KV>
-__device__ __forceinline__ u32x4 dequant8_bf16(u32x2 w, float scale) {
+__device__ __forceinline__ u32x4 dequant8_bf16(uint32_t w0, uint32_t w1, float scale) {
   u32x4 r;
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    float f0, f1, f2, f3;
-    code_pair_to_f32<KV, false>(w[h], f0, f1);
-    code_pair_to_f32<KV, true>(w[h], f2, f3);
-    r[2 * h] = pack_bf16x2(f0 * scale, f1 * scale);
-    r[2 * h + 1] = pack_bf16x2(f2 * scale, f3 * scale);
-  }
+  float f0, f1, f2, f3;
+  code_pair_to_f32<KV, false>(w0, f0, f1);
+  code_pair_to_f32<KV, true>(w0, f2, f3);
+  r[0] = pack_bf16x2(f0 * scale, f1 * scale);
+  r[1] = pack_bf16x2(f2 * scale, f3 * scale);
+  code_pair_to_f32<KV, false>(w1, f0, f1);
+  code_pair_to_f32<KV, true>(w1, f2, f3);
+  r[2] = pack_bf16x2(f0 * scale, f1 * scale);
+  r[3] = pack_bf16x2(f2 * scale, f3 * scale);
   return r;
 }
 
 template <int KV>
-__device__ __forceinline__ void prefill_fill_store(const FillRegs<KV>& R, uint16_t* Ks, uint16_t* Vt,
-                                                   int tid) {
-  const int lane = tid & 63, w = tid >> 6;
-  const int kc = tid & 15;
+__device__ __forceinline__ void fill_store(const Fill<KV>& F, uint16_t* Ks, uint16_t* Vs) {
+  const int tid = threadIdx.x;
+  const u32x4 zero = {0, 0, 0, 0};
+  if constexpr (KV == NVS_DTYPE_BF16) {
+    const int c = tid & 15;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int key = (tid >> 4) + 16 * i;
-    u32x4 val;
-    if constexpr (KV == NVS_DTYPE_BF16)
-      val = R.k[i];
-    else
-      val = dequant8_bf16<KV>(R.k[i], R.ksc[i]);
-    *reinterpret_cast<u32x4*>(Ks + key * kKStride + 8 * kc) = val;
-  }
-  const int kg = lane & 15, vc = 4 * w + (lane >> 4);
-  u32x4 v[4];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    if constexpr (KV == NVS_DTYPE_BF16)
-      v[e] = R.v[e];
-    else
-      v[e] = dequant8_bf16<KV>(R.v[e], R.vsc[e]);
-  }
-  // 4 keys x 8 d -> 8 d-rows x 4 keys.
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
-    u32x2 t;
-    t[0] = __builtin_amdgcn_perm(v[1][j >> 1], v[0][j >> 1], sel);
-    t[1] = __builtin_amdgcn_perm(v[3][j >> 1], v[2][j >> 1], sel);
-    *reinterpret_cast<u32x2*>(Vt + (8 * vc + j) * kVStride + 4 * kg) = t;
+    for (int i = 0; i < 2; ++i) {
+      const int key = (tid >> 4) + 32 * i;
+      *reinterpret_cast<u32x4*>(Ks + tile_at(key, 8 * c)) = F.ok[i] ? F.k[i] : zero;
+      *reinterpret_cast<u32x4*>(Vs + tile_at(key, 8 * c)) = F.ok[i] ? F.v[i] : zero;
+    }
+  } else {
+    const int key = tid >> 3, c = tid & 7;
+    const u32x4 kc = F.ok ? F.k : zero, vc = F.ok ? F.v : zero;
+    const float ks = F.ok ? F.ks : 0.0f, vs = F.ok ? F.vs : 0.0f;
+    *reinterpret_cast<u32x4*>(Ks + tile_at(key, 16 * c)) = dequant8_bf16<KV>(kc[0], kc[1], ks);
+    *reinterpret_cast<u32x4*>(Ks + tile_at(key, 16 * c + 8)) = dequant8_bf16<KV>(kc[2], kc[3], ks);
+    *reinterpret_cast<u32x4*>(Vs + tile_at(key, 16 * c)) = dequant8_bf16<KV>(vc[0], vc[1], vs);
+    *reinterpret_cast<u32x4*>(Vs + tile_at(key, 16 * c + 8)) = dequant8_bf16<KV>(vc[2], vc[3], vs);
   }
 }
 
-// One work item: (sequence b, query tile qt, query head hkv * g + cg).  Every
-// thread of the work-group runs the same items, so the barriers inside match.
+// Block ids of logical blocks [win0, win0 + kBlockWindow) of sequence b, -1
+// where the table has none, the block is outside the pool or past the keys
+// the item reads.
+__device__ __forceinline__ void load_block_window(const PrefillArgs& a, int b, int win0, int kv_end,
+                                                  int* blk_lds) {
+  for (int i = threadIdx.x; i < kBlockWindow; i += kThreads) {
+    const int lb = win0 + i;
+    int blk = -1;
+    if ((int64_t)lb * a.bs < kv_end && lb < a.bt_stride) blk = a.bt[(int64_t)b * a.bt_stride + lb];
+    blk_lds[i] = (blk >= 0 && blk < a.NB) ? blk : -1;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// One 64-key tile for one wave's 32 query positions.
+// Lane (qc = lane % 32, h = lane / 32).  S^T accumulator t, register v holds
+// key 32 t + 8 (v / 4) + 4 h + v % 4 for query qc; O^T accumulator n,
+// register v holds d = 32 n + 8 (v / 4) + 4 h + v % 4.
+// ---------------------------------------------------------------------------
+constexpr float kLazyRescale = 8.0f;  // log2 units; p stays below 2^8
+
+__device__ __forceinline__ void tile_compute(const uint16_t* Ks, const uint16_t* Vs, const bf16x8 (&qop)[8],
+                                             f32x16 (&o)[4], float& m_run, float& l_run, int kt,
+                                             int lim, bool need_mask, float scale_log2) {
+  const int lane = threadIdx.x & 63;
+  const int qc = lane & 31, h = lane >> 5;
+  // ---- S^T = K . Q^T ------------------------------------------------------
+  f32x16 s[2];
+  s[0] = f32x16{};
+  s[1] = f32x16{};
+  const int ksw = swz(qc);  // swz(32 t + qc) == swz(qc)
+#pragma unroll
+  for (int st = 0; st < 8; ++st) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const bf16x8 kop =
+          *reinterpret_cast<const bf16x8*>(Ks + (32 * t + qc) * kHeadDim + (((2 * st + h) ^ ksw) << 3));
+      s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop, qop[st], s[t], 0, 0, 0);
+    }
+  }
+  // ---- online softmax (log2 domain); a query's 64 keys sit in one lane pair
+  float mx = -INFINITY;
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      float x = s[t][v] * scale_log2;
+      if (need_mask) {
+        const int key = kt + 32 * t + 8 * (v >> 2) + 4 * h + (v & 3);
+        x = key <= lim ? x : -INFINITY;
+      }
+      s[t][v] = x;
+      mx = fmaxf(mx, x);
+    }
+  mx = fmaxf(mx, shfl_xor(mx, 32));
+  if (__any(mx > m_run + kLazyRescale)) {
+    const float m_new = fmaxf(m_run, mx);
+    const float alpha = fast_exp2(m_run - (m_new == -INFINITY ? 0.0f : m_new));
+    m_run = m_new;
+    l_run *= alpha;
+#pragma unroll
+    for (int n = 0; n < 4; ++n) o[n] *= alpha;
+  }
+  const float ms = m_run == -INFINITY ? 0.0f : m_run;
+  // ---- O^T += V^T . P^T, 16 keys per MFMA ----------------------------------
+  // Slice m covers keys 16m + 4h + 0..3 and 16m + 8 + 4h + 0..3 (the P^T
+  // registers 8 (m % 2) .. + 7 of accumulator m / 2).  Its V^T operand at
+  // d = 32n + lane % 32 takes two transposing reads: lane (r, c) of a 16-lane
+  // group supplies key 16m + 4h + r (+ 8), d = 32n + 16 (lane / 16 % 2) + 4c.
+  const int r = (lane >> 2) & 3, c = lane & 3;
+  const int dq = 16 * ((lane >> 4) & 1) + 4 * c;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const int t = m >> 1, v0 = 8 * (m & 1);
+    float p[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      p[e] = fast_exp2(s[t][v0 + e] - ms);
+      l_run += p[e];
+    }
+    u32x4 pw;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) pw[e] = pack_bf16x2(p[2 * e], p[2 * e + 1]);
+    const bf16x8 pop = __builtin_bit_cast(bf16x8, pw);
+    const int key0 = 16 * m + 4 * h + r;
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+      const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (i16x4 __attribute__((address_space(3)))*)(Vs + tile_at(key0, 32 * n + dq)));
+      const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (i16x4 __attribute__((address_space(3)))*)(Vs + tile_at(key0 + 8, 32 * n + dq)));
+      const i16x8 vv = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      o[n] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, vv), pop, o[n], 0, 0, 0);
+    }
+  }
+}
+
+// One work item: (sequence b, position tile qt, kv head hkv, head group hg).
+// Every thread of the work-group runs the same items, so the barriers match.
 template <int KV, bool PAGED>
-__device__ __forceinline__ void prefill_item(const PrefillArgs& a, int b, int qt, int hkv, int cg,
-                                             uint16_t* Ks, uint16_t* Vt) {
-  const int hq = hkv * a.g + cg;
+__device__ __forceinline__ void prefill_item(const PrefillArgs& a, int b, int qt, int hkv, int hg,
+                                             uint16_t* lds, int* blk_lds) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int qc = lane & 31, h = lane >> 5;
   const int q0 = a.cu_q[b];
   const int L = a.cu_q[b + 1] - q0;
-  const int m0 = qt * kBM;
-  if (m0 >= L) return;
-  const int k0 = a.cu_k[b];
-  const int K = a.cu_k[b + 1] - k0;
-  const int off = K - L;
-  const int kv_end = min(K, m0 + kBM + off);
+  const int p0 = qt * a.plan.pbm;
+  if (p0 >= L) return;
+  ItemKV it;
+  it.b = b;
+  it.hkv = hkv;
+  it.k0 = a.cu_k[b];
+  it.K = a.cu_k[b + 1] - it.k0;
+  it.win0 = 0;
+  const int off = it.K - L;
+  const int p_last = min(L, p0 + a.plan.pbm) - 1;
+  const int kv_end = min(it.K, p_last + off + 1);
   const int ntiles = kv_end > 0 ? (kv_end + kBN - 1) / kBN : 0;
 
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int col = lane & 15, grp = lane >> 4;
-  const int wrow0 = m0 + 32 * w;  // first query row of this wave
-  const bool wave_active = wrow0 < L;
-  const int wave_last_key = min(K - 1, wrow0 + 31 + off);
+  const int hsub = w % a.hpw, pblk = w / a.hpw;
+  const int hin = hg * kWaves + hsub;
+  const int hq = hkv * a.g + hin;
+  const int wp0 = p0 + kRows * pblk;
+  const bool wave_active = pblk < a.nblk && hin < a.g && wp0 < L;
+  const int my_p = wp0 + qc;
+  const int wave_last_key = min(it.K - 1, min(L - 1, wp0 + kRows - 1) + off);
 
-  // Q^T operands: column = query row wrow0 + 16 c + col, d = 32 grp + 8 s.
-  bf16x8 qop[2][4];
+  // Q^T operand: column = query position my_p, d = 16 s + 8 h + 0..7 (read
+  // unconditionally from a clamped row and head, then zeroed if unused).
+  bf16x8 qop[8];
+  {
+    const bool qok = wave_active && my_p < L;
+    const uint16_t* qp = a.q + (int64_t)(q0 + min(my_p, L - 1)) * a.q_ts +
+                         (int64_t)min(hq, a.Hq - 1) * a.q_hs + 8 * h;
 #pragma unroll
-  for (int c = 0; c < 2; ++c) {
-    const int row = wrow0 + 16 * c + col;
-    if (row < L) {
-      const uint16_t* qp = a.q + (int64_t)(q0 + row) * a.q_ts + (int64_t)hq * a.q_hs + 32 * grp;
-#pragma unroll
-      for (int s = 0; s < 4; ++s) qop[c][s] = *reinterpret_cast<const bf16x8*>(qp + 8 * s);
-    } else {
-#pragma unroll
-      for (int s = 0; s < 4; ++s) qop[c][s] = __builtin_bit_cast(bf16x8, u32x4{0, 0, 0, 0});
+    for (int st = 0; st < 8; ++st) {
+      const u32x4 x = *reinterpret_cast<const u32x4*>(qp + 16 * st);
+      qop[st] = __builtin_bit_cast(bf16x8, qok ? x : u32x4{0, 0, 0, 0});
     }
   }
-
-  f32x4 o[8][2];
+  f32x16 o[4];
 #pragma unroll
-  for (int n = 0; n < 8; ++n) o[n][0] = o[n][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
+  for (int n = 0; n < 4; ++n) o[n] = f32x16{};
+  float m_run = -INFINITY, l_run = 0.0f;
 
-  FillRegs<KV> R;
-  if (ntiles > 0) {
-    prefill_fill_load<KV, PAGED>(R, a, b, hkv, k0, K, 0, tid);
-    prefill_fill_store<KV>(R, Ks, Vt, tid);
-  }
+  if constexpr (PAGED) load_block_window(a, b, 0, kv_end, blk_lds);
   __syncthreads();
-
-  for (int it = 0; it < ntiles; ++it) {
-    const int kt = it * kBN;
-    const bool more = it + 1 < ntiles;
-    if (more) prefill_fill_load<KV, PAGED>(R, a, b, hkv, k0, K, kt + kBN, tid);
-
+  Fill<KV> F;
+  fill_load<KV, PAGED>(F, a, it, 0, blk_lds);  // all zeros when there is no key
+  fill_store<KV>(F, lds, lds + kTile);
+  __syncthreads();
+  for (int j = 0; j < ntiles; ++j) {
+    const int kt = j * kBN;
+    const bool more = j + 1 < ntiles;
+    if constexpr (PAGED) {
+      const int lb = (kt + kBN) / a.bs;
+      if (more && lb >= it.win0 + kBlockWindow) {
+        __syncthreads();
+        it.win0 = lb;
+        load_block_window(a, b, lb, kv_end, blk_lds);
+        __syncthreads();
+      }
+    }
+    if (more) fill_load<KV, PAGED>(F, a, it, kt + kBN, blk_lds);
     if (wave_active && kt <= wave_last_key) {
-      // ---- S^T = K . Q^T --------------------------------------------------
-      f32x4 sacc[4][2];
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        sacc[t][0] = sacc[t][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          const bf16x8 kop =
-              *reinterpret_cast<const bf16x8*>(Ks + (16 * t + col) * kKStride + 32 * grp + 8 * s);
-          sacc[t][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qop[0][s], sacc[t][0], 0, 0, 0);
-          sacc[t][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qop[1][s], sacc[t][1], 0, 0, 0);
-        }
-      }
-      // ---- online softmax per query row (lane column) --------------------
-      const bool need_mask = kt + kBN - 1 > wrow0 + off;
-      bf16x8 pop[2][2];
-#pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        const int lim = wrow0 + 16 * c + col + off;  // last visible key of this row
-        float sv[16];
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            float x = sacc[t][c][r] * a.scale_log2;
-            if (need_mask) {
-              const int key = kt + 16 * t + 4 * grp + r;
-              x = key <= lim ? x : -INFINITY;
-            }
-            sv[4 * t + r] = x;
-          }
-        float mt = sv[0];
-#pragma unroll
-        for (int e = 1; e < 16; ++e) mt = fmaxf(mt, sv[e]);
-        mt = fmaxf(mt, shfl_xor(mt, 16));
-        mt = fmaxf(mt, shfl_xor(mt, 32));
-        const float m_new = fmaxf(m_run[c], mt);
-        const float m_safe = m_new == -INFINITY ? 0.0f : m_new;
-        const float alpha = fast_exp2(m_run[c] - m_safe);
-        m_run[c] = m_new;
-        l_run[c] *= alpha;
-#pragma unroll
-        for (int n = 0; n < 8; ++n) o[n][c] *= alpha;
-        float pv[16];
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          pv[e] = fast_exp2(sv[e] - m_safe);
-          l_run[c] += pv[e];
-        }
-#pragma unroll
-        for (int uu = 0; uu < 2; ++uu) {
-          u32x4 pw;
-          pw[0] = pack_bf16x2(pv[8 * uu + 0], pv[8 * uu + 1]);
-          pw[1] = pack_bf16x2(pv[8 * uu + 2], pv[8 * uu + 3]);
-          pw[2] = pack_bf16x2(pv[8 * uu + 4], pv[8 * uu + 5]);
-          pw[3] = pack_bf16x2(pv[8 * uu + 6], pv[8 * uu + 7]);
-          pop[c][uu] = __builtin_bit_cast(bf16x8, pw);
-        }
-      }
-      // ---- O^T += V^T . P^T ----------------------------------------------
-#pragma unroll
-      for (int n = 0; n < 8; ++n) {
-#pragma unroll
-        for (int uu = 0; uu < 2; ++uu) {
-          const uint16_t* vr = Vt + (16 * n + col) * kVStride + 32 * uu + 4 * grp;
-          const u32x2 lo = *reinterpret_cast<const u32x2*>(vr);
-          const u32x2 hi = *reinterpret_cast<const u32x2*>(vr + 16);
-          const bf16x8 vop = __builtin_bit_cast(bf16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
-          o[n][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop[0][uu], o[n][0], 0, 0, 0);
-          o[n][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop[1][uu], o[n][1], 0, 0, 0);
-        }
-      }
+      const uint16_t* buf = lds + (j & 1) * 2 * kTile;
+      const bool need_mask = kt + kBN - 1 > wp0 + off;
+      tile_compute(buf, buf + kTile, qop, o, m_run, l_run, kt, my_p + off, need_mask, a.scale_log2);
+    }
+    if (more) {
+      uint16_t* nbuf = lds + ((j + 1) & 1) * 2 * kTile;
+      fill_store<KV>(F, nbuf, nbuf + kTile);
     }
     __syncthreads();
-    if (more) {
-      prefill_fill_store<KV>(R, Ks, Vt, tid);
-      __syncthreads();
-    }
   }
 
   if (!wave_active) return;
+  const float l = l_run + shfl_xor(l_run, 32);
+  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+  if (my_p < L) {
+    uint16_t* op = a.out + (int64_t)(q0 + my_p) * a.out_ts + (int64_t)hq * a.out_hs + 4 * h;
 #pragma unroll
-  for (int c = 0; c < 2; ++c) {
-    float l = l_run[c];
-    l += shfl_xor(l, 16);
-    l += shfl_xor(l, 32);
-    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-    const int row = wrow0 + 16 * c + col;
-    if (row < L) {
-      uint16_t* op = a.out + (int64_t)(q0 + row) * a.out_ts + (int64_t)hq * a.out_hs + 4 * grp;
+    for (int n = 0; n < 4; ++n)
 #pragma unroll
-      for (int n = 0; n < 8; ++n) {
+      for (int jj = 0; jj < 4; ++jj) {
         u32x2 wv;
-        wv[0] = pack_bf16x2(o[n][c][0] * inv, o[n][c][1] * inv);
-        wv[1] = pack_bf16x2(o[n][c][2] * inv, o[n][c][3] * inv);
-        *reinterpret_cast<u32x2*>(op + 16 * n) = wv;
+        wv[0] = pack_bf16x2(o[n][4 * jj] * inv, o[n][4 * jj + 1] * inv);
+        wv[1] = pack_bf16x2(o[n][4 * jj + 2] * inv, o[n][4 * jj + 3] * inv);
+        *reinterpret_cast<u32x2*>(op + 32 * n + 8 * jj) = wv;
       }
-    }
   }
 }
 
-// Persistent, dynamically scheduled: work k maps to (unit u, head-in-group
-// c) with u = (list index, kv head); work with k % 8 == x is claimed from XCD
-// x's counter by the work-groups on XCD x (work-group i runs on XCD i % 8), so
-// the g query heads of a unit run on one XCD and fetch its K/V tiles into that
-// XCD's L2 once, and each XCD's work-groups take the heaviest remaining work
-// first.  The next claim is made while the current item runs.
+// Persistent, dynamically scheduled: unit u = (list entry, kv head, head
+// group); units with u % 8 == x are claimed from XCD x's counter by the
+// work-groups running on XCD x (work-group i runs on XCD i % 8), heaviest
+// remaining first.  The next claim is made while the current item runs.
 template <int KV, bool PAGED>
-__global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[kBN * kKStride];
-  __shared__ __attribute__((aligned(16))) uint16_t Vt[kHeadDim * kVStride];
+__global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * 2 * kTile];  // [buffer][K, V][tile]
+  __shared__ int blk_lds[kBlockWindow];
   __shared__ int s_claim[2];
-  const int units = a.plan.hdr->n_prefill * a.Hkv;
-  const int total = ((units + 7) / 8) * 8 * a.g;
+  const int per_entry = a.Hkv * a.hgroups;
+  const int units = a.plan.hdr->n_prefill * per_entry;
   const int xcd = blockIdx.x & 7;
   int* counter = a.plan.hdr->prefill_next + xcd;
   if (threadIdx.x == 0) s_claim[0] = atomicAdd(counter, 1);
   __syncthreads();
   for (int it = 0;; ++it) {
-    const int c = s_claim[it & 1];
-    const int k = 8 * c + xcd;
-    if (k >= total) break;
+    const int u = 8 * s_claim[it & 1] + xcd;
+    if (u >= units) break;
     int next = 0;
     if (threadIdx.x == 0) next = atomicAdd(counter, 1);
-    const int cg = c % a.g;
-    const int u = 8 * (c / a.g) + xcd;
-    if (u < units) {
-      const int idx = u / a.Hkv;
-      const int hkv = u - idx * a.Hkv;
-      const int item = __builtin_amdgcn_readfirstlane(a.plan.plist[idx]);
-      const int b = item / a.plan.ntq;
-      prefill_item<KV, PAGED>(a, b, item - b * a.plan.ntq, hkv, cg, Ks, Vt);
-    }
+    const int idx = u / per_entry;
+    const int rem = u - idx * per_entry;
+    const int hkv = rem / a.hgroups;
+    const int hg = rem - hkv * a.hgroups;
+    const int item = __builtin_amdgcn_readfirstlane(a.plan.plist[idx]);
+    const int b = item / a.plan.ntq;
+    prefill_item<KV, PAGED>(a, b, item - b * a.plan.ntq, hkv, hg, lds, blk_lds);
     // The claim slot read next iteration was last read two iterations ago,
     // before the barrier below.
     if (threadIdx.x == 0) s_claim[(it + 1) & 1] = next;
@@ -391,15 +429,22 @@ int launch_prefill(const AttnParams& P, const Plan& plan, hipStream_t stream) {
   a.k_ts = P.k_ts; a.k_hs = P.k_hs; a.v_ts = P.v_ts; a.v_hs = P.v_hs;
   a.cu_q = P.cu_q; a.cu_k = P.cu_k;
   a.B = P.B; a.Hq = P.Hq; a.Hkv = P.Hkv; a.g = P.Hq / P.Hkv;
+  a.hpw = prefill_heads_per_item(a.g);
+  a.nblk = kWaves / a.hpw;
+  a.hgroups = prefill_head_groups(a.g);
   a.plan = plan;
   a.scale_log2 = P.softmax_scale * 1.4426950408889634f;
   a.out = (uint16_t*)P.out; a.out_ts = P.out_ts; a.out_hs = P.out_hs;
   if (plan.ntq <= 0 || P.B <= 0) return NVS_OK;
+  if (plan.pbm != kRows * a.nblk) {
+    set_error("prefill: plan tile of %d positions does not match %d heads per kv head", plan.pbm, a.g);
+    return NVS_ERR_INVALID;
+  }
   // One work-group per CU (a multiple of 8), never more than the work there can be.
-  const int64_t upper = (((int64_t)P.B * plan.ntq * P.Hkv + 7) / 8) * 8 * a.g;
+  const int64_t upper = (((int64_t)P.B * plan.ntq * P.Hkv * a.hgroups + 7) / 8) * 8;
   int64_t wgs = std::min<int64_t>(upper, (int64_t)device_slots(1));
   wgs = std::max<int64_t>(8, wgs & ~(int64_t)7);
-  dim3 grid((unsigned)wgs), block(256);
+  dim3 grid((unsigned)wgs), block(kThreads);
   const bool paged = P.bt != nullptr;
   if (!paged) {
     hipLaunchKernelGGL((prefill_kernel<NVS_DTYPE_BF16, false>), grid, block, 0, stream, a);

@@ -56,7 +56,7 @@ __device__ __forceinline__ void row_work(const PlanArgs& a, int b, int& nd, int&
   if (a.paged && ql == 1)
     nd = kl > 0 ? min((kl + kDecodePart - 1) / kDecodePart, a.plan.max_parts) : 1;
   else
-    np = min((ql + kPrefillBM - 1) / kPrefillBM, a.plan.ntq);
+    np = min((ql + a.plan.pbm - 1) / a.plan.pbm, a.plan.ntq);
 }
 
 constexpr int kPlanThreads = 1024;

@@ -187,6 +187,14 @@ def test_workspace_bytes():
     n = lib.nvs_attention_workspace_bytes(64, 1, 8192, 32, 8, 128, 256)
     plan = a256(256 + a256(64 * 32 * 32) + a256(64 * 1 * 4))
     assert n == plan + 64 * 32 * 32 * 130 * 4
-    # prefill tiles of 128 rows
+    # prefill tiles: 32 positions per wave, 8 waves shared by the g query heads
+    # of a kv head -> 64 positions at g = 4, 32 at g >= 8, 256 at g = 1
     n = lib.nvs_attention_workspace_bytes(16, 4096, 256, 32, 8, 128, 256)
-    assert n == a256(256 + a256(16 * 32) + a256(16 * 32 * 4))
+    assert n == a256(256 + a256(16 * 32) + a256(16 * 64 * 4))
+    n = lib.nvs_attention_workspace_bytes(16, 4096, 256, 64, 4, 128, 256)
+    assert n == a256(256 + a256(16 * 32) + a256(16 * 128 * 4))
+    n = lib.nvs_attention_workspace_bytes(16, 4096, 256, 8, 8, 128, 256)
+    assert n == a256(256 + a256(16 * 32) + a256(16 * 16 * 4))
+    # unknown group size (num_kv_heads 0): the smallest tile, an upper bound
+    n = lib.nvs_attention_workspace_bytes(16, 4096, 256, 32, 0, 128, 256)
+    assert n == a256(256 + a256(16 * 32) + a256(16 * 128 * 4))
