@@ -16,6 +16,10 @@ static int validate_common(const AttnParams& P, const char* who) {
               "%s: at most 16 query heads per kv head, got %d", who, P.Hq / P.Hkv);
   NVS_REQUIRE(P.max_seqlen_q >= 0 && P.max_seqlen_k >= 0, NVS_ERR_INVALID,
               "%s: negative max_seqlen", who);
+  // The kernels take the row max of the unscaled scores, which needs a
+  // positive scale (the layer passes head_dim^-0.5).
+  NVS_REQUIRE(P.softmax_scale > 0.0f && P.softmax_scale < INFINITY, NVS_ERR_INVALID,
+              "%s: softmax_scale must be positive and finite, got %g", who, (double)P.softmax_scale);
   NVS_REQUIRE(P.q_ts % 8 == 0 && P.q_hs % 8 == 0 && ((uintptr_t)P.q % 16) == 0, NVS_ERR_INVALID,
               "%s: q rows must be 16-byte aligned", who);
   NVS_REQUIRE(P.out_ts % 8 == 0 && P.out_hs % 8 == 0 && ((uintptr_t)P.out % 16) == 0,

@@ -214,9 +214,16 @@ __device__ __forceinline__ void load_block_window(const PrefillArgs& a, int b, i
 // ---------------------------------------------------------------------------
 constexpr float kLazyRescale = 8.0f;  // log2 units; p stays below 2^8
 
+// MASK: the tile crosses the wave's causal diagonal; key kt + k is visible to
+// this lane's query when k <= rel + 4 h (rel = last visible key - kt - 4 h,
+// so the per-register key offsets are compile-time constants).
+// Scores are scaled inside the exponent: with softmax_scale > 0 the row max
+// of the raw scores scaled is the max of the scaled scores, and
+// p = 2^(s * scale_log2 - m) is one v_fma + one v_exp.
+template <bool MASK>
 __device__ __forceinline__ void tile_compute(const uint16_t* Ks, const uint16_t* Vs, const bf16x8 (&qop)[8],
-                                             f32x16 (&o)[4], float& m_run, float& l_run, int kt,
-                                             int lim, bool need_mask, float scale_log2) {
+                                             f32x16 (&o)[4], float& m_run, float& l_run, int rel,
+                                             float scale_log2) {
   const int lane = threadIdx.x & 63;
   const int qc = lane & 31, h = lane >> 5;
   // ---- S^T = K . Q^T ------------------------------------------------------
@@ -239,15 +246,13 @@ __device__ __forceinline__ void tile_compute(const uint16_t* Ks, const uint16_t*
   for (int t = 0; t < 2; ++t)
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
-      float x = s[t][v] * scale_log2;
-      if (need_mask) {
-        const int key = kt + 32 * t + 8 * (v >> 2) + 4 * h + (v & 3);
-        x = key <= lim ? x : -INFINITY;
+      if constexpr (MASK) {
+        const int k = 32 * t + 8 * (v >> 2) + (v & 3);  // key - kt - 4 h
+        s[t][v] = k <= rel ? s[t][v] : -INFINITY;
       }
-      s[t][v] = x;
-      mx = fmaxf(mx, x);
+      mx = fmaxf(mx, s[t][v]);
     }
-  mx = fmaxf(mx, shfl_xor(mx, 32));
+  mx = fmaxf(mx, shfl_xor(mx, 32)) * scale_log2;
   if (__any(mx > m_run + kLazyRescale)) {
     const float m_new = fmaxf(m_run, mx);
     const float alpha = fast_exp2(m_run - (m_new == -INFINITY ? 0.0f : m_new));
@@ -256,26 +261,25 @@ __device__ __forceinline__ void tile_compute(const uint16_t* Ks, const uint16_t*
 #pragma unroll
     for (int n = 0; n < 4; ++n) o[n] *= alpha;
   }
-  const float ms = m_run == -INFINITY ? 0.0f : m_run;
+  const float nms = m_run == -INFINITY ? 0.0f : -m_run;
   // ---- O^T += V^T . P^T, 16 keys per MFMA ----------------------------------
   // Slice m covers keys 16m + 4h + 0..3 and 16m + 8 + 4h + 0..3 (the P^T
   // registers 8 (m % 2) .. + 7 of accumulator m / 2).  Its V^T operand at
   // d = 32n + lane % 32 takes two transposing reads: lane (r, c) of a 16-lane
   // group supplies key 16m + 4h + r (+ 8), d = 32n + 16 (lane / 16 % 2) + 4c.
+  // The row sum adds the bf16-rounded p, the values the MFMA multiplies.
   const int r = (lane >> 2) & 3, c = lane & 3;
   const int dq = 16 * ((lane >> 4) & 1) + 4 * c;
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
     const int t = m >> 1, v0 = 8 * (m & 1);
-    float p[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      p[e] = fast_exp2(s[t][v0 + e] - ms);
-      l_run += p[e];
-    }
     u32x4 pw;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) pw[e] = pack_bf16x2(p[2 * e], p[2 * e + 1]);
+    for (int e = 0; e < 4; ++e) {
+      pw[e] = pack_bf16x2(fast_exp2(fmaf(s[t][v0 + 2 * e], scale_log2, nms)),
+                          fast_exp2(fmaf(s[t][v0 + 2 * e + 1], scale_log2, nms)));
+      l_run = add_bf16x2(pw[e], l_run);
+    }
     const bf16x8 pop = __builtin_bit_cast(bf16x8, pw);
     const int key0 = 16 * m + 4 * h + r;
 #pragma unroll
@@ -359,8 +363,10 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int b, int qt
     if (more) fill_load<KV, PAGED>(F, a, it, kt + kBN, blk_lds);
     if (wave_active && kt <= wave_last_key) {
       const uint16_t* buf = lds + (j & 1) * 2 * kTile;
-      const bool need_mask = kt + kBN - 1 > wp0 + off;
-      tile_compute(buf, buf + kTile, qop, o, m_run, l_run, kt, my_p + off, need_mask, a.scale_log2);
+      if (kt + kBN - 1 > wp0 + off)  // the tile crosses the wave's diagonal
+        tile_compute<true>(buf, buf + kTile, qop, o, m_run, l_run, my_p + off - kt - 4 * h, a.scale_log2);
+      else
+        tile_compute<false>(buf, buf + kTile, qop, o, m_run, l_run, 0, a.scale_log2);
     }
     if (more) {
       uint16_t* nbuf = lds + ((j + 1) & 1) * 2 * kTile;
