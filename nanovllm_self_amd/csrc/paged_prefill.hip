@@ -82,27 +82,23 @@ __device__ __forceinline__ int tile_at(int key, int d) {
 }
 
 // ---------------------------------------------------------------------------
-// Tile fill: global -> registers (issued a tile ahead) -> swizzled LDS.
-// bf16: thread t owns chunk t % 16 of key rows t / 16 and t / 16 + 32 of K
-// and V.  Codes: thread t owns 16 codes (d = 16 (t % 8) ..) of key row t / 8.
-// Rows past the sequence or in a missing block are zero.
+// Tile fill: global -> registers (issued at the start of an iteration) ->
+// swizzled LDS (stored at its end).  K and V tiles are filled separately:
+// their LDS lifetimes are offset by two tiles.  bf16: thread t owns 16-byte
+// chunk t % 16 of key rows t / 16 and t / 16 + 32; codes: thread t owns 16
+// codes (d = 16 (t % 8) ..) of key row t / 8.  Rows past the sequence or in
+// a missing block are stored as zeros.
 // ---------------------------------------------------------------------------
 template <int KV>
-struct Fill {
-  u32x4 k[2], v[2];
-  bool ok[2];  // row holds a visible key (else stored as zeros)
+struct Half {
+  u32x4 x;
+  float sc;
+  bool ok;  // row holds a visible key (else stored as zeros)
 };
 template <>
-struct Fill<NVS_DTYPE_INT8> {
-  u32x4 k, v;
-  float ks, vs;
-  bool ok;
-};
-template <>
-struct Fill<NVS_DTYPE_FP8_E4M3> {
-  u32x4 k, v;
-  float ks, vs;
-  bool ok;
+struct Half<NVS_DTYPE_BF16> {
+  u32x4 x[2];
+  bool ok[2];
 };
 
 struct ItemKV {
@@ -111,12 +107,12 @@ struct ItemKV {
 };
 
 // Loads are issued unconditionally from in-bounds addresses (a missing block
-// reads block 0, a row outside the local k/v reads its first or last row) and replaced by
-// zeros when stored: with no load behind a branch and no use of the loaded
-// values before the store, the compiler's wait counts stay exact and the
-// compute never waits for the next tile's loads.
-template <int KV, bool PAGED>
-__device__ __forceinline__ void fill_load(Fill<KV>& F, const PrefillArgs& a, const ItemKV& it, int kt,
+// reads block 0, a row outside the local k/v reads its first or last row) and
+// replaced by zeros when stored: with no load behind a branch and no use of
+// the loaded values before the store, the compiler's wait counts stay exact
+// and the compute never waits for a later tile's loads.
+template <int KV, bool PAGED, bool ISV>
+__device__ __forceinline__ void half_load(Half<KV>& F, const PrefillArgs& a, const ItemKV& it, int kt,
                                           const int* blk_lds) {
   const int tid = threadIdx.x;
   int64_t slot0 = 0;
@@ -135,22 +131,22 @@ __device__ __forceinline__ void fill_load(Fill<KV>& F, const PrefillArgs& a, con
       F.ok[i] = have && kt + key < it.K;
       if constexpr (PAGED) {
         const int64_t row = (slot0 + key) * a.Hkv + it.hkv;
-        F.k[i] = *reinterpret_cast<const u32x4*>((const uint16_t*)a.kc + row * kHeadDim + 8 * c);
-        F.v[i] = *reinterpret_cast<const u32x4*>((const uint16_t*)a.vc + row * kHeadDim + 8 * c);
+        const uint16_t* src = (const uint16_t*)(ISV ? a.vc : a.kc);
+        F.x[i] = *reinterpret_cast<const u32x4*>(src + row * kHeadDim + 8 * c);
       } else {
         const int64_t row = max((int64_t)0, min((int64_t)it.k0 + kt + key, a.T - 1));
-        F.k[i] = *reinterpret_cast<const u32x4*>(a.k + row * a.k_ts + (int64_t)it.hkv * a.k_hs + 8 * c);
-        F.v[i] = *reinterpret_cast<const u32x4*>(a.v + row * a.v_ts + (int64_t)it.hkv * a.v_hs + 8 * c);
+        const uint16_t* src = ISV ? a.v + row * a.v_ts + (int64_t)it.hkv * a.v_hs
+                                  : a.k + row * a.k_ts + (int64_t)it.hkv * a.k_hs;
+        F.x[i] = *reinterpret_cast<const u32x4*>(src + 8 * c);
       }
     }
   } else {
     const int key = tid >> 3, c = tid & 7;
     F.ok = have && kt + key < it.K;
     const int64_t row = (slot0 + key) * a.Hkv + it.hkv;
-    F.k = *reinterpret_cast<const u32x4*>((const uint8_t*)a.kc + row * kHeadDim + 16 * c);
-    F.v = *reinterpret_cast<const u32x4*>((const uint8_t*)a.vc + row * kHeadDim + 16 * c);
-    F.ks = a.ks[row];
-    F.vs = a.vs[row];
+    const uint8_t* src = (const uint8_t*)(ISV ? a.vc : a.kc);
+    F.x = *reinterpret_cast<const u32x4*>(src + row * kHeadDim + 16 * c);
+    F.sc = (ISV ? a.vs : a.ks)[row];
   }
 }
 
@@ -171,7 +167,7 @@ __device__ __forceinline__ u32x4 dequant8_bf16(uint32_t w0, uint32_t w1, float s
 }
 
 template <int KV>
-__device__ __forceinline__ void fill_store(const Fill<KV>& F, uint16_t* Ks, uint16_t* Vs) {
+__device__ __forceinline__ void half_store(const Half<KV>& F, uint16_t* S) {
   const int tid = threadIdx.x;
   const u32x4 zero = {0, 0, 0, 0};
   if constexpr (KV == NVS_DTYPE_BF16) {
@@ -179,17 +175,14 @@ __device__ __forceinline__ void fill_store(const Fill<KV>& F, uint16_t* Ks, uint
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int key = (tid >> 4) + 32 * i;
-      *reinterpret_cast<u32x4*>(Ks + tile_at(key, 8 * c)) = F.ok[i] ? F.k[i] : zero;
-      *reinterpret_cast<u32x4*>(Vs + tile_at(key, 8 * c)) = F.ok[i] ? F.v[i] : zero;
+      *reinterpret_cast<u32x4*>(S + tile_at(key, 8 * c)) = F.ok[i] ? F.x[i] : zero;
     }
   } else {
     const int key = tid >> 3, c = tid & 7;
-    const u32x4 kc = F.ok ? F.k : zero, vc = F.ok ? F.v : zero;
-    const float ks = F.ok ? F.ks : 0.0f, vs = F.ok ? F.vs : 0.0f;
-    *reinterpret_cast<u32x4*>(Ks + tile_at(key, 16 * c)) = dequant8_bf16<KV>(kc[0], kc[1], ks);
-    *reinterpret_cast<u32x4*>(Ks + tile_at(key, 16 * c + 8)) = dequant8_bf16<KV>(kc[2], kc[3], ks);
-    *reinterpret_cast<u32x4*>(Vs + tile_at(key, 16 * c)) = dequant8_bf16<KV>(vc[0], vc[1], vs);
-    *reinterpret_cast<u32x4*>(Vs + tile_at(key, 16 * c + 8)) = dequant8_bf16<KV>(vc[2], vc[3], vs);
+    const u32x4 x = F.ok ? F.x : zero;
+    const float sc = F.ok ? F.sc : 0.0f;
+    *reinterpret_cast<u32x4*>(S + tile_at(key, 16 * c)) = dequant8_bf16<KV>(x[0], x[1], sc);
+    *reinterpret_cast<u32x4*>(S + tile_at(key, 16 * c + 8)) = dequant8_bf16<KV>(x[2], x[3], sc);
   }
 }
 
@@ -207,30 +200,20 @@ __device__ __forceinline__ void load_block_window(const PrefillArgs& a, int b, i
 }
 
 // ---------------------------------------------------------------------------
-// One 64-key tile for one wave's 32 query positions.
+// One wave's 32 query positions against 64-key tiles.
 // Lane (qc = lane % 32, h = lane / 32).  S^T accumulator t, register v holds
 // key 32 t + 8 (v / 4) + 4 h + v % 4 for query qc; O^T accumulator n,
 // register v holds d = 32 n + 8 (v / 4) + 4 h + v % 4.
 // ---------------------------------------------------------------------------
 constexpr float kLazyRescale = 8.0f;  // log2 units; p stays below 2^8
 
-// MASK: the tile crosses the wave's causal diagonal; key kt + k is visible to
-// this lane's query when k <= rel + 4 h (rel = last visible key - kt - 4 h,
-// so the per-register key offsets are compile-time constants).
-// Scores are scaled inside the exponent: with softmax_scale > 0 the row max
-// of the raw scores scaled is the max of the scaled scores, and
-// p = 2^(s * scale_log2 - m) is one v_fma + one v_exp.
-template <bool MASK>
-__device__ __forceinline__ void tile_compute(const uint16_t* Ks, const uint16_t* Vs, const bf16x8 (&qop)[8],
-                                             f32x16 (&o)[4], float& m_run, float& l_run, int rel,
-                                             float scale_log2) {
+// S^T = K . Q^T (16 MFMAs).
+__device__ __forceinline__ void qk_tile(const uint16_t* Ks, const bf16x8 (&qop)[8], f32x16 (&s)[2]) {
   const int lane = threadIdx.x & 63;
   const int qc = lane & 31, h = lane >> 5;
-  // ---- S^T = K . Q^T ------------------------------------------------------
-  f32x16 s[2];
+  const int ksw = swz(qc);  // swz(32 t + qc) == swz(qc)
   s[0] = f32x16{};
   s[1] = f32x16{};
-  const int ksw = swz(qc);  // swz(32 t + qc) == swz(qc)
 #pragma unroll
   for (int st = 0; st < 8; ++st) {
 #pragma unroll
@@ -240,47 +223,20 @@ __device__ __forceinline__ void tile_compute(const uint16_t* Ks, const uint16_t*
       s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop, qop[st], s[t], 0, 0, 0);
     }
   }
-  // ---- online softmax (log2 domain); a query's 64 keys sit in one lane pair
-  float mx = -INFINITY;
-#pragma unroll
-  for (int t = 0; t < 2; ++t)
-#pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      if constexpr (MASK) {
-        const int k = 32 * t + 8 * (v >> 2) + (v & 3);  // key - kt - 4 h
-        s[t][v] = k <= rel ? s[t][v] : -INFINITY;
-      }
-      mx = fmaxf(mx, s[t][v]);
-    }
-  mx = fmaxf(mx, shfl_xor(mx, 32)) * scale_log2;
-  if (__any(mx > m_run + kLazyRescale)) {
-    const float m_new = fmaxf(m_run, mx);
-    const float alpha = fast_exp2(m_run - (m_new == -INFINITY ? 0.0f : m_new));
-    m_run = m_new;
-    l_run *= alpha;
-#pragma unroll
-    for (int n = 0; n < 4; ++n) o[n] *= alpha;
-  }
-  const float nms = m_run == -INFINITY ? 0.0f : -m_run;
-  // ---- O^T += V^T . P^T, 16 keys per MFMA ----------------------------------
-  // Slice m covers keys 16m + 4h + 0..3 and 16m + 8 + 4h + 0..3 (the P^T
-  // registers 8 (m % 2) .. + 7 of accumulator m / 2).  Its V^T operand at
-  // d = 32n + lane % 32 takes two transposing reads: lane (r, c) of a 16-lane
-  // group supplies key 16m + 4h + r (+ 8), d = 32n + 16 (lane / 16 % 2) + 4c.
-  // The row sum adds the bf16-rounded p, the values the MFMA multiplies.
-  const int r = (lane >> 2) & 3, c = lane & 3;
+}
+
+// O^T += V^T . P^T (16 MFMAs, 16 keys each).  P^T slice m = keys 16m + 4h +
+// 0..3 and 16m + 8 + 4h + 0..3 (registers 8 (m % 2) .. + 7 of S^T accumulator
+// m / 2).  Its V^T operand at d = 32n + lane % 32 takes two transposing
+// reads: lane (r, c) of a 16-lane group supplies key 16m + 4h + r (+ 8),
+// d = 32n + 16 (lane / 16 % 2) + 4c.
+__device__ __forceinline__ void pv_tile(const uint16_t* Vs, const u32x4 (&pw)[4], f32x16 (&o)[4]) {
+  const int lane = threadIdx.x & 63;
+  const int h = lane >> 5, r = (lane >> 2) & 3, c = lane & 3;
   const int dq = 16 * ((lane >> 4) & 1) + 4 * c;
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
-    const int t = m >> 1, v0 = 8 * (m & 1);
-    u32x4 pw;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      pw[e] = pack_bf16x2(fast_exp2(fmaf(s[t][v0 + 2 * e], scale_log2, nms)),
-                          fast_exp2(fmaf(s[t][v0 + 2 * e + 1], scale_log2, nms)));
-      l_run = add_bf16x2(pw[e], l_run);
-    }
-    const bf16x8 pop = __builtin_bit_cast(bf16x8, pw);
+    const bf16x8 pop = __builtin_bit_cast(bf16x8, pw[m]);
     const int key0 = 16 * m + 4 * h + r;
 #pragma unroll
     for (int n = 0; n < 4; ++n) {
@@ -294,8 +250,93 @@ __device__ __forceinline__ void tile_compute(const uint16_t* Ks, const uint16_t*
   }
 }
 
+// One pipelined step of a wave (iteration j of the tile loop):
+//   block 1: O += V_{j-1}^T P_{j-1}^T (PV) beside the row max of S_j (SM);
+//   then the lazy rescale of O and l when the max moved;
+//   block 2: S_{j+1} = K_{j+1} Q^T (QK) beside P_j = 2^(S_j scale - m) (SM).
+// Each block's MFMAs and VALU work are independent, so they overlap.
+// MASK: tile j crosses the wave's causal diagonal; key kt + k is visible to
+// this lane's query when k <= rel + 4 h (rel = last visible key - kt - 4 h,
+// so the per-register key offsets are compile-time constants).
+// Scores are scaled inside the exponent: with softmax_scale > 0 the row max
+// of the raw scores scaled is the max of the scaled scores, and
+// p = 2^(s * scale_log2 - m) is one v_fma + one v_exp.  The row sum adds the
+// bf16-rounded p, the values the MFMA multiplies.
+template <bool MASK, bool PV, bool QK, bool SM>
+__device__ __forceinline__ void step(const uint16_t* Vp, const uint16_t* Kn, const bf16x8 (&qop)[8],
+                                     f32x16 (&sc)[2], f32x16 (&sn)[2], u32x4 (&pw)[4], f32x16 (&o)[4],
+                                     float& m_run, float& l_run, int rel, float scale_log2) {
+  if constexpr (PV) pv_tile(Vp, pw, o);
+  if constexpr (SM) {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        if constexpr (MASK) {
+          const int k = 32 * t + 8 * (v >> 2) + (v & 3);  // key - kt - 4 h
+          sc[t][v] = k <= rel ? sc[t][v] : -INFINITY;
+        }
+        mx = fmaxf(mx, sc[t][v]);
+      }
+    mx = fmaxf(mx, shfl_xor(mx, 32)) * scale_log2;
+    if (__any(mx > m_run + kLazyRescale)) {
+      const float m_new = fmaxf(m_run, mx);
+      const float alpha = fast_exp2(m_run - (m_new == -INFINITY ? 0.0f : m_new));
+      m_run = m_new;
+      l_run *= alpha;
+#pragma unroll
+      for (int n = 0; n < 4; ++n) o[n] *= alpha;
+    }
+  }
+  if constexpr (QK) qk_tile(Kn, qop, sn);
+  if constexpr (SM) {
+    const float nms = m_run == -INFINITY ? 0.0f : -m_run;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const int t = m >> 1, v0 = 8 * (m & 1);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        pw[m][e] = pack_bf16x2(fast_exp2(fmaf(sc[t][v0 + 2 * e], scale_log2, nms)),
+                               fast_exp2(fmaf(sc[t][v0 + 2 * e + 1], scale_log2, nms)));
+        l_run = add_bf16x2(pw[m][e], l_run);
+      }
+    }
+  }
+}
+
+// Iteration j of a wave whose last tile with a visible key is lt (-1: none).
+__device__ __forceinline__ void wave_iteration(int j, int lt, bool mask, const uint16_t* Vp, const uint16_t* Kn,
+                                               const bf16x8 (&qop)[8], f32x16 (&sc)[2], f32x16 (&sn)[2],
+                                               u32x4 (&pw)[4], f32x16 (&o)[4], float& m_run, float& l_run,
+                                               int rel, float scale_log2) {
+  const bool pv = j >= 1 && j - 1 <= lt, qk = j + 1 <= lt, sm = j <= lt;
+#define NVS_STEP(M, P, Q, S) step<M, P, Q, S>(Vp, Kn, qop, sc, sn, pw, o, m_run, l_run, rel, scale_log2)
+  if (pv && qk && sm) {
+    if (mask) NVS_STEP(true, true, true, true); else NVS_STEP(false, true, true, true);
+  } else if (sm) {
+    if (pv) {
+      if (mask) NVS_STEP(true, true, false, true); else NVS_STEP(false, true, false, true);
+    } else if (qk) {
+      if (mask) NVS_STEP(true, false, true, true); else NVS_STEP(false, false, true, true);
+    } else {
+      if (mask) NVS_STEP(true, false, false, true); else NVS_STEP(false, false, false, true);
+    }
+  } else if (pv) {
+    NVS_STEP(false, true, false, false);
+  }
+#undef NVS_STEP
+}
+
 // One work item: (sequence b, position tile qt, kv head hkv, head group hg).
-// Every thread of the work-group runs the same items, so the barriers match.
+// Every thread of the work-group runs the same items and iterations, so the
+// barriers match.
+//
+// Software pipeline over 64-key tiles, one barrier per iteration.
+// Iteration j reads V_{j-1} (Vbuf[(j-1) % 2]) and K_{j+1} (Kbuf[(j+1) % 2]);
+// its fill loads K_{j+2} and V_j at the start and stores them into Kbuf[j % 2]
+// and Vbuf[j % 2] at the end, buffers whose tiles (K_j, V_{j-2}) were last
+// read in iteration j - 1, before the previous barrier.
 template <int KV, bool PAGED>
 __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int b, int qt, int hkv, int hg,
                                              uint16_t* lds, int* blk_lds) {
@@ -323,6 +364,8 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int b, int qt
   const bool wave_active = pblk < a.nblk && hin < a.g && wp0 < L;
   const int my_p = wp0 + qc;
   const int wave_last_key = min(it.K - 1, min(L - 1, wp0 + kRows - 1) + off);
+  // Last tile with a key visible to this wave (-1: none).
+  const int lt = (wave_active && wave_last_key >= 0) ? wave_last_key / kBN : -1;
 
   // Q^T operand: column = query position my_p, d = 16 s + 8 h + 0..7 (read
   // unconditionally from a clamped row and head, then zeroed if unused).
@@ -341,38 +384,50 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int b, int qt
 #pragma unroll
   for (int n = 0; n < 4; ++n) o[n] = f32x16{};
   float m_run = -INFINITY, l_run = 0.0f;
+  f32x16 s0[2], s1[2];
+  u32x4 pw[4];
 
+  uint16_t* const Kb = lds;              // Kbuf[2]
+  uint16_t* const Vb = lds + 2 * kTile;  // Vbuf[2]
+  // Fill tiles are clamped to the item's last tile, so every iteration issues
+  // the same loads and stores; a clamped tile lands in a buffer that is not
+  // read again.
+  const int last_kt = max(ntiles - 1, 0) * kBN;
   if constexpr (PAGED) load_block_window(a, b, 0, kv_end, blk_lds);
   __syncthreads();
-  Fill<KV> F;
-  fill_load<KV, PAGED>(F, a, it, 0, blk_lds);  // all zeros when there is no key
-  fill_store<KV>(F, lds, lds + kTile);
+  Half<KV> FK, FV;
+  half_load<KV, PAGED, false>(FK, a, it, 0, blk_lds);  // all zeros when there is no key
+  half_load<KV, PAGED, false>(FV, a, it, min(kBN, last_kt), blk_lds);
+  half_store<KV>(FK, Kb);
+  half_store<KV>(FV, Kb + kTile);
   __syncthreads();
-  for (int j = 0; j < ntiles; ++j) {
-    const int kt = j * kBN;
-    const bool more = j + 1 < ntiles;
+  if (lt >= 0) qk_tile(Kb, qop, s0);
+  __syncthreads();
+
+  // One iteration; S_j lives in sc, S_{j+1} is produced into sn.
+  auto iteration = [&](int j, f32x16(&sc)[2], f32x16(&sn)[2]) {
     if constexpr (PAGED) {
-      const int lb = (kt + kBN) / a.bs;
-      if (more && lb >= it.win0 + kBlockWindow) {
-        __syncthreads();
-        it.win0 = lb;
-        load_block_window(a, b, lb, kv_end, blk_lds);
+      if (j + 2 < ntiles && ((j + 2) * kBN) / a.bs >= it.win0 + kBlockWindow) {
+        // Every read of the old window happened before the last barrier.
+        it.win0 = (j * kBN) / a.bs;
+        load_block_window(a, b, it.win0, kv_end, blk_lds);
         __syncthreads();
       }
     }
-    if (more) fill_load<KV, PAGED>(F, a, it, kt + kBN, blk_lds);
-    if (wave_active && kt <= wave_last_key) {
-      const uint16_t* buf = lds + (j & 1) * 2 * kTile;
-      if (kt + kBN - 1 > wp0 + off)  // the tile crosses the wave's diagonal
-        tile_compute<true>(buf, buf + kTile, qop, o, m_run, l_run, my_p + off - kt - 4 * h, a.scale_log2);
-      else
-        tile_compute<false>(buf, buf + kTile, qop, o, m_run, l_run, 0, a.scale_log2);
-    }
-    if (more) {
-      uint16_t* nbuf = lds + ((j + 1) & 1) * 2 * kTile;
-      fill_store<KV>(F, nbuf, nbuf + kTile);
-    }
+    half_load<KV, PAGED, false>(FK, a, it, min((j + 2) * kBN, last_kt), blk_lds);
+    half_load<KV, PAGED, true>(FV, a, it, min(j * kBN, last_kt), blk_lds);
+    const int kt = j * kBN;
+    const bool mask = kt + kBN - 1 > wp0 + off;  // tile j crosses the wave's diagonal
+    wave_iteration(j, lt, mask, Vb + ((j - 1) & 1) * kTile, Kb + ((j + 1) & 1) * kTile, qop, sc, sn, pw, o,
+                   m_run, l_run, my_p + off - kt - 4 * h, a.scale_log2);
+    half_store<KV>(FK, Kb + (j & 1) * kTile);
+    half_store<KV>(FV, Vb + (j & 1) * kTile);
     __syncthreads();
+  };
+  for (int j = 0; j <= ntiles; j += 2) {
+    iteration(j, s0, s1);
+    if (j + 1 > ntiles) break;
+    iteration(j + 1, s1, s0);
   }
 
   if (!wave_active) return;
@@ -398,7 +453,7 @@ __device__ __forceinline__ void prefill_item(const PrefillArgs& a, int b, int qt
 // remaining first.  The next claim is made while the current item runs.
 template <int KV, bool PAGED>
 __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * 2 * kTile];  // [buffer][K, V][tile]
+  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * 2 * kTile];  // Kbuf[2], Vbuf[2]
   __shared__ int blk_lds[kBlockWindow];
   __shared__ int s_claim[2];
   const int per_entry = a.Hkv * a.hgroups;
