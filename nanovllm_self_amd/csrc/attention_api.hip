@@ -1,5 +1,7 @@
 // C ABI of the attention kernels: argument validation and dispatch of decode
 // rows (q_len == 1, split-K decode) and prefill rows (MFMA flash prefill).
+#include <algorithm>
+
 #include "nvs_common.h"
 #include "attention_common.h"
 
@@ -40,17 +42,27 @@ static int prefill_tiles(int max_seqlen_q, int pbm) {
   return t < 1 ? 1 : t;
 }
 
+// Query heads per kv head (1 when the pair is invalid: sizing only).
+static int group_of(int num_heads, int num_kv_heads) {
+  return (num_kv_heads > 0 && num_heads % num_kv_heads == 0) ? num_heads / num_kv_heads : 1;
+}
+
 int64_t attention_workspace_bytes(int num_seqs, int max_seqlen_q, int max_seqlen_k, int num_heads,
                                   int num_kv_heads) {
   if (num_seqs <= 0 || num_heads <= 0) return 0;
-  const int parts = decode_max_parts(max_seqlen_k);
+  const int waves = decode_wave_cap(num_seqs, max_seqlen_k, num_kv_heads);
   const int ntq = prefill_tiles(max_seqlen_q, prefill_pbm(num_heads, num_kv_heads));
-  return align256(plan_bytes(num_seqs, parts, ntq)) + decode_workspace_bytes(num_seqs, max_seqlen_k, num_heads);
+  return align256(plan_bytes(num_seqs, waves, ntq)) +
+         decode_workspace_bytes(waves, group_of(num_heads, num_kv_heads));
 }
 
 static Plan make_plan(void* ws, const AttnParams& P) {
   const int pbm = prefill_pbm(P.Hq, P.Hkv);
-  return plan_at(ws, P.B, decode_max_parts(P.max_seqlen_k), prefill_tiles(P.max_seqlen_q, pbm), pbm);
+  return plan_at(ws, P.B, decode_wave_cap(P.B, P.max_seqlen_k, P.Hkv), prefill_tiles(P.max_seqlen_q, pbm), pbm);
+}
+
+int decode_launch_waves(const Plan& plan) {
+  return std::min(plan.max_waves, device_slots(4 * kDecodeWavesPerEU));
 }
 }  // namespace nvs
 
@@ -113,15 +125,19 @@ extern "C" int nvs_paged_attention(const void* q, int64_t q_tok_stride, int64_t 
               NVS_ERR_INVALID,
               "paged_attention: block_tables rows (%lld) too short for max_seqlen_k %d",
               (long long)bt_stride, max_seqlen_k);
+  NVS_REQUIRE((int64_t)num_seqs * num_kv_heads * (((int64_t)max_seqlen_k + kDecodeTile - 1) / kDecodeTile) <
+                  (1ll << 31),
+              NVS_ERR_UNSUPPORTED, "paged_attention: batch too large for one call (decode units exceed 2^31)");
   if (max_seqlen_q <= 0) return NVS_OK;
   rc = check_workspace(P, "paged_attention");
   if (rc != NVS_OK) return rc;
   hipStream_t s = (hipStream_t)stream;
   const Plan plan = make_plan(workspace, P);
-  char* partials = (char*)workspace + align256(plan_bytes(num_seqs, plan.max_parts, plan.ntq));
-  rc = launch_plan(P, plan, /*paged=*/true, s);
+  char* partials = (char*)workspace + align256(plan_bytes(num_seqs, plan.max_waves, plan.ntq));
+  const int waves = decode_launch_waves(plan);
+  rc = launch_plan(P, plan, /*paged=*/true, waves, s);
   if (rc != NVS_OK) return rc;
-  rc = launch_decode(P, plan, partials, s);
+  rc = launch_decode(P, plan, waves, partials, s);
   if (rc != NVS_OK || max_seqlen_q == 1) return rc;
   return launch_prefill(P, plan, s);
 }
@@ -160,7 +176,7 @@ extern "C" int nvs_varlen_attention(const void* q, int64_t q_tok_stride, int64_t
   if (rc != NVS_OK) return rc;
   hipStream_t s = (hipStream_t)stream;
   const Plan plan = make_plan(workspace, P);
-  rc = launch_plan(P, plan, /*paged=*/false, s);
+  rc = launch_plan(P, plan, /*paged=*/false, 0, s);
   if (rc != NVS_OK) return rc;
   return launch_prefill(P, plan, s);
 }

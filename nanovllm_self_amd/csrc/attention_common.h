@@ -6,23 +6,13 @@
 namespace nvs {
 
 constexpr int kHeadDim = 128;    // head_dim served by the attention kernels
-#ifndef NVS_DECODE_PART
-#define NVS_DECODE_PART 256
-#endif
-constexpr int kDecodePart = NVS_DECODE_PART;  // keys per decode wave (one split-K partition)
-#ifndef NVS_DECODE_BUFFERS
-#define NVS_DECODE_BUFFERS 2
-#endif
-constexpr int kDecodeBuffers = NVS_DECODE_BUFFERS;  // decode tile ring depth (>= 2)
 #ifndef NVS_DECODE_WAVES_PER_EU
 #define NVS_DECODE_WAVES_PER_EU 2
 #endif
-constexpr int kDecodeWavesPerEU = NVS_DECODE_WAVES_PER_EU;  // occupancy floor requested
-
-inline int decode_max_parts(int max_seqlen_k) {
-  const int p = (max_seqlen_k + kDecodePart - 1) / kDecodePart;
-  return p < 1 ? 1 : p;
-}
+constexpr int kDecodeWavesPerEU = NVS_DECODE_WAVES_PER_EU;  // decode waves per SIMD
+constexpr int kDecodeTile = 32;         // keys per decode tile (one unit of decode work)
+constexpr int kDecodeMaxWaves = 2048;   // decode waves per call at most (256 CUs x 8)
+constexpr int kDecodeMinUnits = 4;      // fewest units a decode wave is given
 
 // 2^x on the hardware transcendental unit (v_exp_f32); 2^-inf = 0.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -75,16 +65,18 @@ __device__ __forceinline__ bf16x8 codes8_to_bf16x8(uint32_t lo, uint32_t hi) {
 
 // ---------------------------------------------------------------------------
 // Work plan.  A one-work-group planning kernel turns cu_seqlens into compact
-// work lists in the workspace, so the attention kernels launch a fixed,
-// persistent grid and never dispatch empty work-groups (each costs the
-// dispatcher several nanoseconds; an upper-bound grid is mostly empty on
-// ragged batches).
-//   decode records: one DecodeItem per (q_len == 1 row, 256-key partition),
-//                 self-contained (row, key range and the partition's block
-//                 ids), so a decode wave starts an item with one load that
-//                 it issued during the previous item instead of a chain of
-//                 dependent cu_seqlens / block-table loads; a row with no
-//                 visible key gets one record.
+// work lists in the workspace, on the device, so the attention kernels
+// launch a fixed persistent grid and never dispatch empty work-groups (each
+// costs the dispatcher several nanoseconds; an upper-bound grid is mostly
+// empty on ragged batches).
+//   decode rows:  one DecodeRow per q_len == 1 row of a paged call with at
+//                 least one visible key (the plan zeroes the others).  Decode
+//                 work is counted in units, one per (row, kv head, 32-key
+//                 tile), ordered row-major, then kv head, then tile.  A
+//                 unit range [s_w, e_w) with s_w = floor(w U / W) goes to
+//                 decode wave w of W (stream-K: every wave gets the same
+//                 number of units and streams across row boundaries).
+//   wave starts:  the (row, kv head, tile) of each wave's first unit.
 //   prefill list: b * ntq + qt, one entry per (q_len > 1 row, tile of
 //                 prefill_positions(g) query positions), every row's tiles in
 //                 descending qt (heaviest first).
@@ -101,55 +93,68 @@ __host__ __device__ inline int prefill_positions(int g) {
 }
 __host__ __device__ inline int prefill_head_groups(int g) { return (g + kPrefillWaves - 1) / kPrefillWaves; }
 
-// Block ids a decode partition can span (block_size >= 64).
-constexpr int kDecodeItemBlocks = kDecodePart / 64;
-
-struct DecodeItem {
-  int q0;    // query / output row
-  int b;     // sequence (row of cu_seqlens)
-  int p;     // partition: keys [p * kDecodePart, kend)
-  int kend;  // min((p + 1) * kDecodePart, k_len); k_len (<= 0) for a row without keys
-  int blk[kDecodeItemBlocks];  // block ids of the partition's blocks in order,
-                               // -1 where the table has none or it is outside the pool
+struct DecodeRow {
+  int b;       // sequence (row of cu_seqlens)
+  int q0;      // query / output row
+  int K;       // visible keys (k_len)
+  int n;       // 32-key tiles, ceil(K / 32); 0 for a row without keys
+  int prefix;  // first unit of the row: sum over earlier rows of Hkv * n
+  int pad[3];
 };
-constexpr int kDecodeItemWords = (int)(sizeof(DecodeItem) / 4);
-static_assert(sizeof(DecodeItem) % 16 == 0, "decode records are read in 16-byte units");
+static_assert(sizeof(DecodeRow) == 32, "decode rows are 32 bytes");
+
+struct WaveStart {
+  int row, h, t, pad;  // decode row index, kv head and tile of the wave's first unit
+};
 
 struct PlanHeader {
-  int n_decode;
-  int n_prefill;
+  int n_rows;           // decode rows
+  int n_units;          // decode units U
+  int n_waves;          // decode waves W with work (W <= U)
+  int n_prefill;        // prefill list entries
   int prefill_next[8];  // per-XCD work counters of the prefill kernel (zeroed by the plan)
-  int pad[54];          // keeps the lists 256-byte aligned
+  int pad[52];          // keeps the lists 256-byte aligned
 };
 static_assert(sizeof(PlanHeader) == 256, "plan header is one 256-byte line");
 
 struct Plan {
   PlanHeader* hdr;
-  DecodeItem* drec;
+  DecodeRow* rows;
+  WaveStart* starts;
   int* plist;
-  int max_parts;  // decode partitions per sequence (bound of the record list)
+  int max_waves;  // decode waves the call may use (bound of the start list and the partials)
   int ntq;        // prefill query tiles per sequence (list stride)
   int pbm;        // query positions per prefill tile
 };
 
 inline int64_t align256(int64_t x) { return (x + 255) & ~(int64_t)255; }
 
-inline int64_t decode_records_bytes(int B, int max_parts) {
-  return align256((int64_t)B * max_parts * (int64_t)sizeof(DecodeItem));
+// Decode waves a call may use: at most kDecodeMaxWaves, and no more than the
+// units there can be (B rows x Hkv heads x ceil(max_seqlen_k / 32) tiles)
+// allow at kDecodeMinUnits each.
+inline int decode_wave_cap(int B, int max_seqlen_k, int Hkv) {
+  const int64_t units = (int64_t)B * (Hkv > 0 ? Hkv : 1) * ((max_seqlen_k + kDecodeTile - 1) / kDecodeTile);
+  const int64_t w = (units + kDecodeMinUnits - 1) / kDecodeMinUnits;
+  return (int)(w < 1 ? 1 : (w > kDecodeMaxWaves ? kDecodeMaxWaves : w));
 }
 
 // Bytes of the plan for a batch; it sits at the start of the workspace.
-inline int64_t plan_bytes(int B, int max_parts, int ntq) {
-  return (int64_t)sizeof(PlanHeader) + decode_records_bytes(B, max_parts) + align256((int64_t)B * ntq * 4);
+inline int64_t plan_bytes(int B, int max_waves, int ntq) {
+  return (int64_t)sizeof(PlanHeader) + align256((int64_t)B * sizeof(DecodeRow)) +
+         align256((int64_t)max_waves * sizeof(WaveStart)) + align256((int64_t)B * ntq * 4);
 }
 
-inline Plan plan_at(void* ws, int B, int max_parts, int ntq, int pbm) {
+inline Plan plan_at(void* ws, int B, int max_waves, int ntq, int pbm) {
   Plan p;
   char* c = (char*)ws;
   p.hdr = (PlanHeader*)c;
-  p.drec = (DecodeItem*)(c + sizeof(PlanHeader));
-  p.plist = (int*)(c + sizeof(PlanHeader) + decode_records_bytes(B, max_parts));
-  p.max_parts = max_parts;
+  c += sizeof(PlanHeader);
+  p.rows = (DecodeRow*)c;
+  c += align256((int64_t)B * sizeof(DecodeRow));
+  p.starts = (WaveStart*)c;
+  c += align256((int64_t)max_waves * sizeof(WaveStart));
+  p.plist = (int*)c;
+  p.max_waves = max_waves;
   p.ntq = ntq;
   p.pbm = pbm;
   return p;
@@ -191,11 +196,14 @@ struct AttnParams {
   int64_t ws_bytes;
 };
 
-int64_t decode_workspace_bytes(int num_seqs, int max_seqlen_k, int num_heads);
+int64_t decode_workspace_bytes(int max_waves, int group);
 int64_t attention_workspace_bytes(int num_seqs, int max_seqlen_q, int max_seqlen_k, int num_heads,
                                   int num_kv_heads);
-int launch_plan(const AttnParams& P, const Plan& plan, bool paged, hipStream_t stream);
-int launch_decode(const AttnParams& P, const Plan& plan, void* partials, hipStream_t stream);
+// Decode waves a paged call launches: its workspace bound and the device's
+// resident wave slots, whichever is smaller.
+int decode_launch_waves(const Plan& plan);
+int launch_plan(const AttnParams& P, const Plan& plan, bool paged, int decode_waves, hipStream_t stream);
+int launch_decode(const AttnParams& P, const Plan& plan, int waves, void* partials, hipStream_t stream);
 int launch_prefill(const AttnParams& P, const Plan& plan, hipStream_t stream);
 
 }  // namespace nvs

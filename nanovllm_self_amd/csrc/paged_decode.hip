@@ -5,9 +5,12 @@
 // (:441-498): out[h] = softmax(q[h] . K^T * scale) V over the sequence's
 // k_len cached keys, kv head h / (Hq / Hkv).
 //
-// Work decomposition: one wave64 per (sequence, kv head, partition of
-// kPart keys).  The wave serves every query head of its kv head, so each
-// K/V byte is read from HBM exactly once.  Per 32-key tile:
+// Work decomposition (stream-K): decode work is counted in units, one per
+// (row, kv head, 32-key tile), ordered row, then kv head, then tile; wave w
+// of W processes units [floor(w U / W), floor((w + 1) U / W)) as one
+// continuous stream, so every wave has the same work and the load pipeline
+// never restarts at item boundaries.  A wave serves every query head of a kv
+// head, so each K/V byte is read from HBM exactly once.  Per 32-key tile:
 //   S^T[32 keys x 16 heads] = K[32 x 128] . Q^T   (8 x mfma_f32_16x16x32_bf16)
 //   O^T[128 x 16 heads]    += V^T[128 x 32] . P^T (8 x mfma_f32_16x16x32_bf16)
 // With keys as the MFMA row index, the S^T accumulator layout (lane = head
@@ -16,10 +19,12 @@
 // 256-byte coalescing and transposed in registers with v_perm_b32.  Quantised
 // codes are converted to bf16 exactly in registers (int8 and e4m3 values are
 // bf16-representable); the per-key scales multiply S (K) and P (V).
-// Each wave writes a partial (m, l, o[128]) per head; decode_reduce_kernel
-// merges the partitions with a log-sum-exp (a second launch: the kernel
-// boundary makes the partials visible across XCDs without device-scope
-// fences, which on a multi-XCD part write back the L2).
+// A (row, kv head) pair that lies inside one wave's range is normalised and
+// written by that wave; a pair split across waves leaves one partial
+// (m, l, o[128]) per head in each wave, merged by decode_merge_kernel with a
+// log-sum-exp (a second launch: the kernel boundary makes the partials
+// visible across XCDs without device-scope fences, which on a multi-XCD part
+// write back the L2).
 #include <algorithm>
 
 #include "nvs_common.h"
@@ -34,18 +39,13 @@ struct DecodeArgs {
   const void* vc;
   const float* ks;
   const float* vs;
-  const int32_t* cu_q;
-  const int32_t* cu_k;
-  const int32_t* bt;
-  int bt_stride;  // row stride == number of columns (32-bit: keeps the
-  int NB;         // block-table lookup a scalar compare + scalar load)
-  int64_t T;      // query / output rows
+  int bt_stride;  // row stride == number of columns
+  int NB;
   int Hq, Hkv, g, bs;
-  int max_parts;
   float scale_log2;
-  float* ws_o;   // [B, Hq, max_parts, 128]
-  float* ws_ml;  // [B, Hq, max_parts, 2]
-  Plan plan;
+  float* ws_o;   // [max_waves, 2 slots, g, 128]
+  float* ws_ml;  // [max_waves, 2 slots, g, 2]
+  PlanHeader* hdr;
   uint16_t* out;
   int64_t out_ts, out_hs;
 };
@@ -84,13 +84,13 @@ constexpr int kKStepStride = (KV == NVS_DTYPE_BF16) ? 32 : 8;
 template <int KV>
 constexpr int kKGroupStride = (KV == NVS_DTYPE_BF16) ? 8 : 32;
 
-// Per-lane byte offsets from a tile's first row, identical for every tile:
-// loads take a wave-uniform 64-bit base (scalar registers) plus these 32-bit
-// lane offsets, so no per-load address arithmetic remains in the loop.
+// Per-lane byte offsets from a tile's first row, identical for every tile.
+// A load of slot e adds the wave-uniform offset of key row slot_key(e, 0)
+// (or 16 t) to a scalar base, so each kind of load needs one lane offset.
 struct LaneOffsets {
-  uint32_t k[2];   // key 16t + col, d = 8 grp (bf16) / 32 grp (codes)
-  uint32_t v[8];   // key slot_key(e), d = 8 col
-  uint32_t sc[8];  // scale of key slot_key(e)
+  uint32_t k;   // key col, d = 8 grp (bf16) / 32 grp (codes)
+  uint32_t v;   // key 4 grp, d = 8 col
+  uint32_t sc;  // scale of key 4 grp
 };
 
 template <int KV>
@@ -98,73 +98,46 @@ __device__ __forceinline__ LaneOffsets lane_offsets(int Hkv, int col, int grp) {
   constexpr uint32_t ESZ = (KV == NVS_DTYPE_BF16) ? 2 : 1;
   const uint32_t row = (uint32_t)Hkv * kHeadDim * ESZ;  // bytes per token row (all heads)
   LaneOffsets o;
-#pragma unroll
-  for (int t = 0; t < 2; ++t) o.k[t] = (uint32_t)(16 * t + col) * row + kKGroupStride<KV> * grp * ESZ;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    o.v[e] = (uint32_t)slot_key(e, grp) * row + 8 * col * ESZ;
-    o.sc[e] = (uint32_t)slot_key(e, grp) * Hkv * 4;
-  }
+  o.k = (uint32_t)col * row + kKGroupStride<KV> * grp * ESZ;
+  o.v = (uint32_t)(4 * grp) * row + 8 * col * ESZ;
+  o.sc = (uint32_t)(4 * grp) * Hkv * 4;
   return o;
 }
 
-// One decode work item as the wave holds it: scalars plus the block ids of
-// the partition in a vector value (a private array here would be placed in
-// LDS and re-read per tile).
-typedef int idxvec __attribute__((ext_vector_type(kDecodeItemBlocks)));
-
-struct ItemRegs {
-  int q0, b, p, kend;
-  int lb0;      // logical block of the partition's first key
-  idxvec blk;   // -1: missing block
-};
-
-// Scalars of a record from its words.
-__device__ __forceinline__ ItemRegs unpack_item(const int (&w)[kDecodeItemWords], int bs) {
-  ItemRegs it;
-  it.q0 = w[0];
-  it.b = w[1];
-  it.p = w[2];
-  it.kend = w[3];
-  it.lb0 = it.p * kDecodePart / bs;
-#pragma unroll
-  for (int j = 0; j < kDecodeItemBlocks; ++j) it.blk[j] = w[4 + j];
-  return it;
-}
-
+// Loads of one 32-key tile of kv head h whose first key sits at offset koff
+// of pool block blk (-1: missing; the loads then read block 0, in bounds).
 template <int KV>
 __device__ __forceinline__ void decode_load(DecodeTile<KV>& T, const DecodeArgs& a, const LaneOffsets& lo,
-                                            const ItemRegs& it, int h, int kt) {
+                                            int blk, int koff, int h) {
   constexpr int ESZ = (KV == NVS_DTYPE_BF16) ? 2 : 1;
-  const int lblk = kt / a.bs;
-  const int j = lblk - it.lb0;
-  int blk = it.blk[0];
-#pragma unroll
-  for (int i = 1; i < kDecodeItemBlocks; ++i) blk = (j == i) ? it.blk[i] : blk;
-  T.has = blk >= 0;  // the plan stores -1 for missing and out-of-pool blocks
-  const int64_t row0 = ((int64_t)(T.has ? blk : 0) * a.bs + (kt - lblk * a.bs)) * a.Hkv + h;
+  T.has = blk >= 0;
+  const int64_t row0 = ((int64_t)(T.has ? blk : 0) * a.bs + koff) * a.Hkv + h;
+  const int64_t rowb = (int64_t)a.Hkv * kHeadDim * ESZ;  // bytes per token row
   const char* kb = (const char*)a.kc + row0 * kHeadDim * ESZ;
   const char* vb = (const char*)a.vc + row0 * kHeadDim * ESZ;
   if constexpr (KV == NVS_DTYPE_BF16) {
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int s = 0; s < 4; ++s) T.k[t][s] = *reinterpret_cast<const u32x4*>(kb + lo.k[t] + 64 * s);
+      for (int s = 0; s < 4; ++s)
+        T.k[t][s] = *reinterpret_cast<const u32x4*>(kb + 16 * t * rowb + 64 * s + lo.k);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) T.v[e] = *reinterpret_cast<const u32x4*>(vb + lo.v[e]);
+    for (int e = 0; e < 8; ++e)
+      T.v[e] = *reinterpret_cast<const u32x4*>(vb + slot_key(e, 0) * rowb + lo.v);
   } else {
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      T.k[t][0] = *reinterpret_cast<const u32x4*>(kb + lo.k[t]);
-      T.k[t][1] = *reinterpret_cast<const u32x4*>(kb + lo.k[t] + 16);
+      T.k[t][0] = *reinterpret_cast<const u32x4*>(kb + 16 * t * rowb + lo.k);
+      T.k[t][1] = *reinterpret_cast<const u32x4*>(kb + 16 * t * rowb + 16 + lo.k);
     }
     const char* ksb = (const char*)(a.ks + row0);
     const char* vsb = (const char*)(a.vs + row0);
+    const int64_t srow = (int64_t)a.Hkv * 4;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      T.v[e] = *reinterpret_cast<const u32x2*>(vb + lo.v[e]);
-      T.ksc[e] = *reinterpret_cast<const float*>(ksb + lo.sc[e]);
-      T.vsc[e] = *reinterpret_cast<const float*>(vsb + lo.sc[e]);
+      T.v[e] = *reinterpret_cast<const u32x2*>(vb + slot_key(e, 0) * rowb + lo.v);
+      T.ksc[e] = *reinterpret_cast<const float*>(ksb + slot_key(e, 0) * srow + lo.sc);
+      T.vsc[e] = *reinterpret_cast<const float*>(vsb + slot_key(e, 0) * srow + lo.sc);
     }
   }
 }
@@ -326,239 +299,274 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-// One work item: (decode sequence, kv head h, partition), as planned.
-template <int KV, int NBUF>
-__device__ __forceinline__ void paged_decode_item(const DecodeArgs& a, const ItemRegs& it, int h) {
-  const int lane = threadIdx.x;
-  const int q0 = it.q0, b = it.b, p = it.p;
-  const int kbeg = p * kDecodePart;
-  if (kbeg >= it.kend) {
-    if (p == 0 && a.max_parts == 1) {  // no visible key: output 0 (the merge handles max_parts > 1)
-      for (int i = lane; i < a.g * (kHeadDim / 2); i += 64) {
-        const int c = i / (kHeadDim / 2), d = 2 * (i % (kHeadDim / 2));
-        *reinterpret_cast<uint32_t*>(a.out + (int64_t)q0 * a.out_ts + (int64_t)(h * a.g + c) * a.out_hs + d) = 0u;
-      }
-    }
-    return;
-  }
-  const int kend = it.kend;
-  const int ntiles = (kend - kbeg + 31) >> 5;
-  const int col = lane & 15, grp = lane >> 4;
+// Position of a decode wave in its unit stream: a decode row, a kv head and
+// a tile.  All members are wave-uniform (scalar registers).
+struct Cursor {
+  int row;             // decode row index
+  int b, q0, K, n;     // that row (DecodeRow)
+  int h, t;            // kv head, tile
+};
 
-  // Q^T as the B operand: column = head (col < g); step s, lane group grp
-  // holds the same 8 d values as the K operand: d = 32 s + 8 grp for bf16
-  // caches, 32 grp + 8 s for code caches.
-  bf16x8 qop[4];
-  if (col < a.g) {
-    const uint16_t* qp = a.q + (int64_t)q0 * a.q_ts + (int64_t)(h * a.g + col) * a.q_hs +
-                         kKGroupStride<KV> * grp;
+__device__ __forceinline__ void set_row(Cursor& c, const DecodeRow& r, int row) {
+  c.row = row;
+  c.b = r.b;
+  c.q0 = r.q0;
+  c.K = r.K;
+  c.n = r.n;
+}
+
+// Block id of cursor c's tile (-1 where the table has none or it is outside
+// the pool); a 32-key tile never spans two blocks (block_size % 64 == 0).
+__device__ __forceinline__ int tile_block(const DecodeArgs& a, const int32_t* __restrict__ bt, const Cursor& c) {
+  const int lb = (c.t * kDecodeTile) / a.bs;
+  const int blk = lb < a.bt_stride ? bt[(int64_t)c.b * a.bt_stride + lb] : -1;
+  return (blk >= 0 && blk < a.NB) ? blk : -1;
+}
+
+// Q^T as the B operand for query row q0, kv head h: column = head (col < g);
+// step s, lane group grp holds the same 8 d values as the K operand: d = 32 s
+// + 8 grp for bf16 caches, 32 grp + 8 s for code caches.
+template <int KV>
+__device__ __forceinline__ void load_q(bf16x8 (&qop)[4], const DecodeArgs& a, int q0, int h, int col, int grp) {
+  const bool use = col < a.g;
+  const uint16_t* qp = a.q + (int64_t)q0 * a.q_ts + (int64_t)(h * a.g + (use ? col : 0)) * a.q_hs +
+                       kKGroupStride<KV> * grp;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) qop[s] = *reinterpret_cast<const bf16x8*>(qp + kKStepStride<KV> * s);
+  for (int s = 0; s < 4; ++s) {
+    const u32x4 x = *reinterpret_cast<const u32x4*>(qp + kKStepStride<KV> * s);
+    qop[s] = __builtin_bit_cast(bf16x8, use ? x : u32x4{0, 0, 0, 0});
+  }
+}
+
+// The end of a (row, kv head) segment: a pair the wave saw whole is normalised
+// and written; a split pair leaves its partial in slot `slot` of wave w.
+// Lane (col, grp) holds O[hq][d] for d = 32 grp + 8 r + j in o[j][r].
+__device__ __forceinline__ void finish_segment(const DecodeArgs& a, const Cursor& c, bool whole, int w, int slot,
+                                               const f32x4 (&o)[8], float m_run, float l_run, int col, int grp) {
+  if (col >= a.g) return;
+  if (whole) {
+    const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+    uint16_t* op = a.out + (int64_t)c.q0 * a.out_ts + (int64_t)(c.h * a.g + col) * a.out_hs + 32 * grp;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      u32x4 v;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) v[m] = pack_bf16x2(o[2 * m][r] * inv, o[2 * m + 1][r] * inv);
+      *reinterpret_cast<u32x4*>(op + 8 * r) = v;
+    }
   } else {
-#pragma unroll
-    for (int s = 0; s < 4; ++s) qop[s] = __builtin_bit_cast(bf16x8, u32x4{0, 0, 0, 0});
-  }
-
-  f32x4 o[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) o[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY, l_run = 0.0f;
-
-  // Ring of NBUF tiles, fully unrolled over the partition so every buffer
-  // index is a compile-time constant: NBUF - 1 tiles are in flight while one
-  // is consumed.
-  // The scheduling barriers keep each tile's loads in issue order: the
-  // hardware's load counter retires in order, so a later tile's load hoisted
-  // above an earlier one would make the wait for the earlier tile drain it too.
-  // Loads are issued unconditionally (tiles past the end re-read the last
-  // tile, an L2 hit) so that every path issues the same loads in the same
-  // order and each wait covers exactly the tile about to be used.
-  constexpr int NT = kDecodePart / 32;
-  const LaneOffsets lo = lane_offsets<KV>(a.Hkv, col, grp);
-  DecodeTile<KV> ring[NBUF];
-  const int last = ntiles - 1;
-#pragma unroll
-  for (int i = 0; i < NBUF - 1; ++i) {
-    decode_load<KV>(ring[i], a, lo, it, h, kbeg + 32 * min(i, last));
-    __builtin_amdgcn_sched_barrier(0);
-  }
-#pragma unroll
-  for (int i = 0; i < NT; ++i) {
-    if (i + NBUF - 1 < NT)
-      decode_load<KV>(ring[(i + NBUF - 1) % NBUF], a, lo, it, h, kbeg + 32 * min(i + NBUF - 1, last));
-    __builtin_amdgcn_sched_barrier(0);
-    if (i < last) {  // every tile but the last is full: no masking
-      if (!ring[i % NBUF].has) zero_tile(ring[i % NBUF]);
-      decode_tile_compute<KV, false>(ring[i % NBUF], qop, o, m_run, l_run, kbeg + 32 * i, kend, grp,
-                                     a.scale_log2);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-  }
-  // The last tile (possibly partial) runs the masked path; its ring slot is
-  // last % NBUF (later clamped loads only re-read the same tile).
-#pragma unroll
-  for (int r = 0; r < NBUF; ++r) {
-    if (last % NBUF == r) {
-      if (!ring[r].has) zero_tile(ring[r]);
-      decode_tile_compute<KV, true>(ring[r], qop, o, m_run, l_run, kbeg + 32 * last, kend, grp,
-                                    a.scale_log2);
-    }
-  }
-  l_run += shfl_xor(l_run, 16);
-  l_run += shfl_xor(l_run, 32);
-
-  if (a.max_parts == 1) {
-    // Single partition: normalise and write the output here.
-    if (col < a.g) {
-      const int hq = h * a.g + col;
-      const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
-      uint16_t* op = a.out + (int64_t)q0 * a.out_ts + (int64_t)hq * a.out_hs + 32 * grp;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        u32x4 w;
-#pragma unroll
-        for (int m = 0; m < 4; ++m) w[m] = pack_bf16x2(o[2 * m][r] * inv, o[2 * m + 1][r] * inv);
-        *reinterpret_cast<u32x4*>(op + 8 * r) = w;
-      }
-    }
-    return;
-  }
-  // Lane (col, grp) holds O[hq][d] for d = 32 grp + 8 r + j.
-  if (col < a.g) {
-    const int hq = h * a.g + col;
-    const int64_t base = ((int64_t)b * a.Hq + hq) * a.max_parts + p;
+    const int64_t base = ((int64_t)w * 2 + slot) * a.g + col;
     float* op = a.ws_o + base * kHeadDim + 32 * grp;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       *reinterpret_cast<f32x4*>(op + 8 * r) = f32x4{o[0][r], o[1][r], o[2][r], o[3][r]};
       *reinterpret_cast<f32x4*>(op + 8 * r + 4) = f32x4{o[4][r], o[5][r], o[6][r], o[7][r]};
     }
-    if (grp == 0) {
-      a.ws_ml[base * 2] = m_run;
-      a.ws_ml[base * 2 + 1] = l_run;
-    }
+    if (grp == 0) *reinterpret_cast<f32x2*>(a.ws_ml + base * 2) = f32x2{m_run, l_run};
   }
 }
 
-// Persistent: each wave walks the plan's decode records with a grid stride,
-// kv head fastest, so the Hkv waves reading one block's rows run side by
-// side.  The next item's record is loaded while the current item runs: it
-// comes through the scalar cache (the restrict-qualified pointer lets the
-// compiler prove no store of this kernel clobbers it), so waiting for it never
-// waits for this wave's vector loads or stores.
+// One decode wave: the units [floor(w U / W), floor((w + 1) U / W)) of the
+// plan, streamed tile by tile.  Cursor c is the tile being computed, n1 the
+// next one (its loads are in flight during c's compute) and n2 the one after
+// (its block id is fetched during c's compute).  Loads are issued
+// unconditionally (past the wave's last unit the cursors stop advancing, so
+// the surplus loads re-read the last tile) and the two-tile ring is unrolled
+// so every buffer index is a compile-time constant.  Row, block-table and
+// start records are read through restrict-qualified pointers, so they are
+// scalar loads whose waits never wait for the wave's vector loads.
 template <int KV>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kDecodeWavesPerEU)))
-void paged_decode_kernel(DecodeArgs a, const int* __restrict__ rec_words) {
-  const int total = a.plan.hdr->n_decode * a.Hkv;
-  int k = blockIdx.x;
-  if (k >= total) return;
-  int w[kDecodeItemWords];
-  const int* r = rec_words + (int64_t)(k / a.Hkv) * kDecodeItemWords;
-#pragma unroll
-  for (int i = 0; i < kDecodeItemWords; ++i) w[i] = r[i];
-  for (; k < total; k += gridDim.x) {
-    const int h = k % a.Hkv;
-    const ItemRegs it = unpack_item(w, a.bs);
-    const int kn = min(k + (int)gridDim.x, total - 1);
-    r = rec_words + (int64_t)(kn / a.Hkv) * kDecodeItemWords;
-#pragma unroll
-    for (int i = 0; i < kDecodeItemWords; ++i) w[i] = r[i];
-    paged_decode_item<KV, kDecodeBuffers>(a, it, h);
-  }
-}
+void paged_decode_kernel(DecodeArgs a, const DecodeRow* __restrict__ rows, const WaveStart* __restrict__ starts,
+                         const int32_t* __restrict__ bt) {
+  const int w = blockIdx.x;
+  const int W = a.hdr->n_waves;
+  if (w >= W) return;
+  const int U = a.hdr->n_units;
+  const int nrows = a.hdr->n_rows;
+  const int s0 = (int)((int64_t)w * U / W);
+  const int left = (int)((int64_t)(w + 1) * U / W) - s0;  // >= 1 (W <= U)
 
-// Log-sum-exp merge of the partitions of every (decode sequence, query
-// head); one wave each.  Lane l owns head_dim elements 2l, 2l + 1.  Partition
-// weights are computed lane-parallel and broadcast with a shuffle, and the
-// partial-output loads are unrolled so many are in flight at once.
-__global__ __launch_bounds__(64) void decode_reduce_kernel(DecodeArgs a) {
-  const int hq = blockIdx.x, b = blockIdx.y;
   const int lane = threadIdx.x;
-  const int q0 = a.cu_q[b];
-  if (a.cu_q[b + 1] - q0 != 1 || q0 < 0 || q0 >= a.T) return;
-  const int klen = a.cu_k[b + 1] - a.cu_k[b];
-  const int parts = klen > 0 ? min((klen + kDecodePart - 1) / kDecodePart, a.max_parts) : 0;
-  const int64_t base = ((int64_t)b * a.Hq + hq) * a.max_parts;
-  const float* ml = a.ws_ml + base * 2;
-  float M = -INFINITY;
-  for (int p = lane; p < parts; p += 64) M = fmaxf(M, ml[2 * p]);
-  M = wave_max(M);
-  float L = 0.0f;
-  for (int p = lane; p < parts; p += 64) L += fast_exp2(ml[2 * p] - M) * ml[2 * p + 1];
-  L = wave_sum(L);
-  const float* po = a.ws_o + base * kHeadDim + 2 * lane;
-  float acc0 = 0.0f, acc1 = 0.0f;
-  for (int p0 = 0; p0 < parts; p0 += 64) {
-    const int n = min(64, parts - p0);
-    const float wl = lane < n ? fast_exp2(ml[2 * (p0 + lane)] - M) : 0.0f;
-    int i = 0;
-    for (; i + 8 <= n; i += 8) {
-      float2 ov[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) ov[u] = *reinterpret_cast<const float2*>(po + (int64_t)(p0 + i + u) * kHeadDim);
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const float w = __shfl(wl, i + u, 64);
-        acc0 += w * ov[u].x;
-        acc1 += w * ov[u].y;
+  const int col = lane & 15, grp = lane >> 4;
+  const LaneOffsets lo = lane_offsets<KV>(a.Hkv, col, grp);
+
+  // Cursors.  nxt holds the row after n2's row, prefetched.
+  Cursor c;
+  {
+    const WaveStart st = starts[w];
+    set_row(c, rows[st.row], st.row);
+    c.h = st.h;
+    c.t = st.t;
+  }
+  DecodeRow nxt = rows[min(c.row + 1, nrows - 1)];
+  auto advance = [&](Cursor& x) {
+    if (++x.t == x.n) {
+      x.t = 0;
+      if (++x.h == a.Hkv) {
+        x.h = 0;
+        set_row(x, nxt, x.row + 1);
+        nxt = rows[min(x.row + 1, nrows - 1)];
       }
     }
-    for (; i < n; ++i) {
-      const float w = __shfl(wl, i, 64);
-      const float2 ov = *reinterpret_cast<const float2*>(po + (int64_t)(p0 + i) * kHeadDim);
-      acc0 += w * ov.x;
-      acc1 += w * ov.y;
+  };
+  Cursor n1 = c;
+  if (left > 1) advance(n1);
+  Cursor n2 = n1;
+  if (left > 2) advance(n2);
+
+  bf16x8 qop[4];
+  load_q<KV>(qop, a, c.q0, c.h, col, grp);
+  f32x4 o[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) o[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.0f;
+  int seg_t0 = c.t;  // first tile of the current segment
+  int slot = 0;      // partial slot of the current segment (0: the wave's first)
+
+  DecodeTile<KV> r0, r1;
+  decode_load<KV>(r0, a, lo, tile_block(a, bt, c), c.t * kDecodeTile % a.bs, c.h);
+  int blk1 = tile_block(a, bt, n1);
+
+  // Tile i (cursor c) from ring slot cur; the loads of tile i + 1 go to nxt_t.
+  auto step = [&](DecodeTile<KV>& cur, DecodeTile<KV>& nxt_t, int i) {
+    decode_load<KV>(nxt_t, a, lo, blk1, n1.t * kDecodeTile % a.bs, n1.h);
+    const int blk2 = tile_block(a, bt, n2);
+    __builtin_amdgcn_sched_barrier(0);
+    if (!cur.has) zero_tile(cur);
+    const int kt = c.t * kDecodeTile;
+    if (kt + kDecodeTile > c.K)  // the row's last, partial tile
+      decode_tile_compute<KV, true>(cur, qop, o, m_run, l_run, kt, c.K, grp, a.scale_log2);
+    else
+      decode_tile_compute<KV, false>(cur, qop, o, m_run, l_run, kt, c.K, grp, a.scale_log2);
+    __builtin_amdgcn_sched_barrier(0);
+    if (c.t == c.n - 1 || i == left - 1) {  // the segment ends with tile i
+      float l = l_run + shfl_xor(l_run, 16);
+      l += shfl_xor(l, 32);
+      finish_segment(a, c, seg_t0 == 0 && c.t == c.n - 1, w, slot, o, m_run, l, col, grp);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      m_run = -INFINITY;
+      l_run = 0.0f;
+      seg_t0 = 0;
+      slot = 1;
+      // The next segment's q (tile i + 1 starts it); its wait falls at tile
+      // i + 1's compute, which waits for that tile's loads anyway.
+      if (i + 1 < left) load_q<KV>(qop, a, n1.q0, n1.h, col, grp);
+    }
+    c = n1;
+    n1 = n2;
+    if (i + 3 < left) advance(n2);
+    blk1 = blk2;
+  };
+  for (int i = 0; i < left; i += 2) {
+    step(r0, r1, i);
+    if (i + 1 >= left) break;
+    step(r1, r0, i + 1);
+  }
+}
+
+// Log-sum-exp merge of the pairs split across waves.  Wave w owns the pair
+// that crosses the boundary after its range if that pair starts inside its
+// range; the pair's partials sit in wave w (slot 0 if the pair is w's first
+// segment, else slot 1) and in waves w + 1 .. w_last (slot 0).  Lane l serves
+// head 4 p + l / 16 of the group (pass p) and head_dim elements 8 (l % 16) ..
+// + 7; one pass over the partials keeps a running max, sum and output, with
+// the loads of four partials in flight at a time.
+__global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a, const DecodeRow* __restrict__ rows,
+                                                         const WaveStart* __restrict__ starts) {
+  const int w = blockIdx.x;
+  const int W = a.hdr->n_waves;
+  if (w + 1 >= W) return;
+  const int U = a.hdr->n_units;
+  const WaveStart st = starts[w + 1];
+  if (st.t == 0) return;  // the boundary falls between pairs
+  const DecodeRow r = rows[st.row];
+  const int first = r.prefix + st.h * r.n;  // the pair's first unit
+  const int sw = (int)((int64_t)w * U / W);
+  if (first < sw) return;  // started in an earlier wave, which merges it
+  const int last = first + r.n - 1;
+  const int w_last = (int)(((int64_t)(last + 1) * W - 1) / U);
+  const int slot_w = first != sw ? 1 : 0;
+  const int lane = threadIdx.x;
+  const int j = lane & 15;
+  for (int c0 = 0; c0 < a.g; c0 += 4) {
+    const int c = c0 + (lane >> 4);
+    const bool use = c < a.g;
+    const int cc = use ? c : 0;
+    float M = -INFINITY, L = 0.0f;
+    f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+    for (int x0 = w; x0 <= w_last; x0 += 4) {
+      f32x2 ml[4];
+      f32x4 o0[4], o1[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int x = min(x0 + u, w_last);
+        const int64_t base = ((int64_t)x * 2 + (x == w ? slot_w : 0)) * a.g + cc;
+        ml[u] = *reinterpret_cast<const f32x2*>(a.ws_ml + base * 2);
+        o0[u] = *reinterpret_cast<const f32x4*>(a.ws_o + base * kHeadDim + 8 * j);
+        o1[u] = *reinterpret_cast<const f32x4*>(a.ws_o + base * kHeadDim + 8 * j + 4);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (x0 + u > w_last) break;
+        const float m_new = fmaxf(M, ml[u][0]);
+        const float al = M == -INFINITY ? 0.0f : fast_exp2(M - m_new);
+        const float be = ml[u][0] == -INFINITY ? 0.0f : fast_exp2(ml[u][0] - m_new);
+        M = m_new;
+        L = L * al + ml[u][1] * be;
+        acc0 = acc0 * al + o0[u] * be;
+        acc1 = acc1 * al + o1[u] * be;
+      }
+    }
+    if (use) {
+      const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+      u32x4 v;
+      v[0] = pack_bf16x2(acc0[0] * inv, acc0[1] * inv);
+      v[1] = pack_bf16x2(acc0[2] * inv, acc0[3] * inv);
+      v[2] = pack_bf16x2(acc1[0] * inv, acc1[1] * inv);
+      v[3] = pack_bf16x2(acc1[2] * inv, acc1[3] * inv);
+      *reinterpret_cast<u32x4*>(a.out + (int64_t)r.q0 * a.out_ts + (int64_t)(st.h * a.g + c) * a.out_hs + 8 * j) = v;
     }
   }
-  const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-  uint16_t* op = a.out + (int64_t)q0 * a.out_ts + (int64_t)hq * a.out_hs + 2 * lane;
-  *reinterpret_cast<uint32_t*>(op) = pack_bf16x2(acc0 * inv, acc1 * inv);
 }
 
-int64_t decode_workspace_bytes(int num_seqs, int max_seqlen_k, int num_heads) {
-  const int64_t parts = decode_max_parts(max_seqlen_k);
-  if (parts <= 1) return 0;
-  return (int64_t)num_seqs * num_heads * parts * (kHeadDim + 2) * (int64_t)sizeof(float);
+int64_t decode_workspace_bytes(int max_waves, int group) {
+  return (int64_t)max_waves * 2 * group * (kHeadDim + 2) * (int64_t)sizeof(float);
 }
 
-int launch_decode(const AttnParams& P, const Plan& plan, void* partials, hipStream_t stream) {
+int launch_decode(const AttnParams& P, const Plan& plan, int waves, void* partials, hipStream_t stream) {
   DecodeArgs a;
   a.q = (const uint16_t*)P.q; a.q_ts = P.q_ts; a.q_hs = P.q_hs;
   a.kc = P.kc; a.vc = P.vc; a.ks = P.ks; a.vs = P.vs;
-  a.cu_q = P.cu_q; a.cu_k = P.cu_k; a.bt = P.bt; a.bt_stride = (int)P.bt_stride; a.NB = (int)P.NB; a.T = P.T;
+  a.bt_stride = (int)P.bt_stride; a.NB = (int)P.NB;
   a.Hq = P.Hq; a.Hkv = P.Hkv; a.g = P.Hq / P.Hkv; a.bs = P.bs;
-  a.max_parts = plan.max_parts;
   a.scale_log2 = P.softmax_scale * 1.4426950408889634f;
   a.out = (uint16_t*)P.out; a.out_ts = P.out_ts; a.out_hs = P.out_hs;
-  a.plan = plan;
-  a.ws_o = nullptr; a.ws_ml = nullptr;
-  if (a.max_parts > 1) {
-    a.ws_o = (float*)partials;
-    a.ws_ml = a.ws_o + (int64_t)P.B * P.Hq * a.max_parts * kHeadDim;
-  }
-  // One wave per SIMD slot (2 per SIMD), never more than the items that can exist.
-  const int64_t upper = (int64_t)P.B * a.max_parts * P.Hkv;
-  const int waves = (int)std::min<int64_t>(upper, device_slots(4 * kDecodeWavesPerEU));
+  a.hdr = plan.hdr;
+  a.ws_o = (float*)partials;
+  a.ws_ml = a.ws_o + (int64_t)plan.max_waves * 2 * a.g * kHeadDim;
+  if (waves <= 0) return NVS_OK;
   dim3 grid(waves), block(64);
-  const int* words = reinterpret_cast<const int*>(plan.drec);
   switch (P.cache_dtype) {
     case NVS_DTYPE_BF16:
-      hipLaunchKernelGGL(paged_decode_kernel<NVS_DTYPE_BF16>, grid, block, 0, stream, a, words);
+      hipLaunchKernelGGL(paged_decode_kernel<NVS_DTYPE_BF16>, grid, block, 0, stream, a, plan.rows, plan.starts, P.bt);
       break;
     case NVS_DTYPE_INT8:
-      hipLaunchKernelGGL(paged_decode_kernel<NVS_DTYPE_INT8>, grid, block, 0, stream, a, words);
+      hipLaunchKernelGGL(paged_decode_kernel<NVS_DTYPE_INT8>, grid, block, 0, stream, a, plan.rows, plan.starts, P.bt);
       break;
     case NVS_DTYPE_FP8_E4M3:
-      hipLaunchKernelGGL(paged_decode_kernel<NVS_DTYPE_FP8_E4M3>, grid, block, 0, stream, a, words);
+      hipLaunchKernelGGL(paged_decode_kernel<NVS_DTYPE_FP8_E4M3>, grid, block, 0, stream, a, plan.rows, plan.starts,
+                         P.bt);
       break;
     default:
       set_error("paged_attention: decode does not serve cache dtype %d", P.cache_dtype);
       return NVS_ERR_UNSUPPORTED;
   }
   int rc = check_launch("paged_decode");
-  if (rc != NVS_OK || a.max_parts == 1) return rc;
-  hipLaunchKernelGGL(decode_reduce_kernel, dim3(P.Hq, P.B), dim3(64), 0, stream, a);
-  return check_launch("decode_reduce");
+  if (rc != NVS_OK || waves < 2) return rc;
+  hipLaunchKernelGGL(decode_merge_kernel, dim3(waves - 1), dim3(64), 0, stream, a, plan.rows, plan.starts);
+  return check_launch("decode_merge");
 }
 
 }  // namespace nvs

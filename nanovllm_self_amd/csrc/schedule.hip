@@ -8,13 +8,13 @@ namespace nvs {
 struct PlanArgs {
   const int32_t* cu_q;
   const int32_t* cu_k;
-  const int32_t* bt;  // paged calls only
-  int64_t bt_stride;
-  int64_t NB;
-  int bs;
   int B;
   int64_t T;
   int paged;
+  int Hq, Hkv;
+  int waves;  // decode waves launched (<= plan.max_waves)
+  uint16_t* out;  // rows without a visible key are zeroed here
+  int64_t out_ts, out_hs;
   Plan plan;
 };
 
@@ -42,11 +42,11 @@ __device__ __forceinline__ int block_scan_1024(int v, int* lds, int& total) {
   return v + before;
 }
 
-// Row b's work counts: decode partitions (q_len == 1 rows of a paged call)
-// or prefill query tiles (every other row); also its first query row and key
-// count.
-__device__ __forceinline__ void row_work(const PlanArgs& a, int b, int& nd, int& np, int& q0, int& kl) {
-  nd = np = 0;
+// Row b's work: a decode row (q_len == 1 row of a paged call) or prefill
+// query tiles (every other row); also its first query row and key count.
+__device__ __forceinline__ void row_work(const PlanArgs& a, int b, bool& dec, int& np, int& q0, int& kl) {
+  dec = false;
+  np = 0;
   q0 = kl = 0;
   if (b >= a.B) return;
   q0 = a.cu_q[b];
@@ -54,7 +54,7 @@ __device__ __forceinline__ void row_work(const PlanArgs& a, int b, int& nd, int&
   kl = a.cu_k[b + 1] - a.cu_k[b];
   if (q0 < 0 || ql <= 0 || (int64_t)q0 + ql > a.T) return;  // malformed rows are skipped
   if (a.paged && ql == 1)
-    nd = kl > 0 ? min((kl + kDecodePart - 1) / kDecodePart, a.plan.max_parts) : 1;
+    dec = true;
   else
     np = min((ql + a.plan.pbm - 1) / a.plan.pbm, a.plan.ntq);
 }
@@ -63,69 +63,93 @@ constexpr int kPlanThreads = 1024;
 constexpr int kPlanWaves = kPlanThreads / 64;
 constexpr int kPlanFastLevels = 512;  // prefill tiles per row the one-pass ordering serves
 
-// The full record of decode entry i of a chunk whose rows' record offsets,
-// first query rows and key counts sit in LDS.
-__device__ __forceinline__ void fill_decode_record(const PlanArgs& a, DecodeItem* rec, int i, int b0,
-                                                   const int* row_off, const int* row_q0,
-                                                   const int* row_kl) {
-  // Row: the last r with row_off[r] <= i (rows without records share the
-  // next row's offset, so they never win).
-  int lo = 0, hi = kPlanThreads - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (row_off[mid] <= i) lo = mid; else hi = mid - 1;
-  }
-  const int p = i - row_off[lo];
-  const int b = b0 + lo, kl = row_kl[lo];
-  const int kbeg = p * kDecodePart;
-  const int kend = kl > 0 ? min(kbeg + kDecodePart, kl) : kl;
-  const int lb0 = kbeg / a.bs;
-  const int lb1 = kend > kbeg ? (kend - 1) / a.bs : lb0 - 1;
-  DecodeItem r;
-  r.q0 = row_q0[lo];
-  r.b = b;
-  r.p = p;
-  r.kend = kend;
-#pragma unroll
-  for (int j = 0; j < kDecodeItemBlocks; ++j) {
-    const int lblk = lb0 + j;
-    int blk = -1;
-    if (lblk <= lb1 && lblk < a.bt_stride) blk = a.bt[(int64_t)b * a.bt_stride + lblk];
-    r.blk[j] = (blk >= 0 && blk < a.NB) ? blk : -1;
-  }
-  *rec = r;
-}
-
 __global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanArgs a) {
   __shared__ int scan_lds[kPlanWaves];
-  __shared__ int row_off[kPlanThreads];
-  __shared__ int row_q0[kPlanThreads];
-  __shared__ int row_kl[kPlanThreads];
+  __shared__ int row_incl[kPlanThreads];  // inclusive unit prefix of the chunk's decode rows
+  __shared__ int row_idx[kPlanThreads];   // decode row index of the chunk's rows
+  __shared__ int row_n[kPlanThreads];     // tiles of the chunk's decode rows
   __shared__ int lev_cnt[kPlanFastLevels * kPlanWaves];
   __shared__ int lev_off[kPlanFastLevels];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const Plan& pl = a.plan;
   if (tid < 8) pl.hdr->prefill_next[tid] = 0;
 
-  // ---- decode records, 1024 rows at a time: scan the rows' partition
-  // counts, stage the rows in LDS, then every thread fills whole records.
-  int base = 0, deepest = 0, np0 = 0;
+  // ---- decode rows, 1024 rows at a time: compact index and unit prefix by
+  // two block scans.  A decode row without a visible key gets no units and no
+  // entry; its output is zeroed here.
+  int nrows = 0, units = 0, deepest = 0, np0 = 0;
   for (int b0 = 0; b0 < a.B; b0 += kPlanThreads) {
-    int nd, np, q0, kl, tot;
-    row_work(a, b0 + tid, nd, np, q0, kl);
+    bool dec;
+    int np, q0, kl, tot_r, tot_u;
+    row_work(a, b0 + tid, dec, np, q0, kl);
     if (b0 == 0) np0 = np;
     deepest = max(deepest, np);
-    const int incl = block_scan_1024(nd, scan_lds, tot);
-    row_off[tid] = incl - nd;
-    row_q0[tid] = q0;
-    row_kl[tid] = kl;
-    __syncthreads();
-    for (int i = tid; i < tot; i += kPlanThreads)
-      fill_decode_record(a, pl.drec + base + i, i, b0, row_off, row_q0, row_kl);
-    base += tot;
-    __syncthreads();
+    const int n = dec && kl > 0 ? (kl + kDecodeTile - 1) / kDecodeTile : 0;
+    const int u = a.Hkv * n;
+    const int ir = block_scan_1024(n > 0 ? 1 : 0, scan_lds, tot_r);
+    const int iu = block_scan_1024(u, scan_lds, tot_u);
+    if (n > 0) {
+      DecodeRow r;
+      r.b = b0 + tid;
+      r.q0 = q0;
+      r.K = kl;
+      r.n = n;
+      r.prefix = units + iu - u;
+      r.pad[0] = r.pad[1] = r.pad[2] = 0;
+      pl.rows[nrows + ir - 1] = r;
+    } else if (dec) {
+      for (int i = 0; i < a.Hq * (kHeadDim / 2); ++i) {
+        const int hq = i / (kHeadDim / 2), d = 2 * (i % (kHeadDim / 2));
+        *reinterpret_cast<uint32_t*>(a.out + (int64_t)q0 * a.out_ts + (int64_t)hq * a.out_hs + d) = 0u;
+      }
+    }
+    nrows += tot_r;
+    units += tot_u;
   }
-  if (tid == 0) pl.hdr->n_decode = base;
+  const int nwaves = units > 0 ? (int)min((int64_t)a.waves, max((int64_t)1, (int64_t)units / kDecodeMinUnits)) : 0;
+  if (tid == 0) {
+    pl.hdr->n_rows = nrows;
+    pl.hdr->n_units = units;
+    pl.hdr->n_waves = nwaves;
+  }
+
+  // ---- wave starts: wave w begins at unit s_w = floor(w U / W), inside the
+  // first row whose inclusive unit prefix exceeds s_w.
+  if (nwaves > 0) {
+    int rbase = 0, ubase = 0;
+    for (int b0 = 0; b0 < a.B; b0 += kPlanThreads) {
+      bool dec;
+      int np, q0, kl, tot_r, tot_u;
+      row_work(a, b0 + tid, dec, np, q0, kl);
+      const int n = dec && kl > 0 ? (kl + kDecodeTile - 1) / kDecodeTile : 0;
+      const int u = a.Hkv * n;
+      const int ir = block_scan_1024(n > 0 ? 1 : 0, scan_lds, tot_r);
+      const int iu = block_scan_1024(u, scan_lds, tot_u);
+      row_incl[tid] = ubase + iu;
+      row_idx[tid] = rbase + ir - 1;
+      row_n[tid] = n;
+      __syncthreads();
+      for (int wv = tid; wv < nwaves; wv += kPlanThreads) {
+        const int sw = (int)((int64_t)wv * units / nwaves);
+        if (sw < ubase || sw >= ubase + tot_u) continue;
+        int lo = 0, hi = kPlanThreads - 1;  // first r with row_incl[r] > sw
+        while (lo < hi) {
+          const int mid = (lo + hi) >> 1;
+          if (row_incl[mid] > sw) hi = mid; else lo = mid + 1;
+        }
+        const int rn = row_n[lo], rel = sw - (row_incl[lo] - a.Hkv * rn);
+        WaveStart st;
+        st.row = row_idx[lo];
+        st.h = rel / rn;
+        st.t = rel - st.h * rn;
+        st.pad = 0;
+        pl.starts[wv] = st;
+      }
+      rbase += tot_r;
+      ubase += tot_u;
+      __syncthreads();
+    }
+  }
 
   // ---- prefill tiles level by level from the deepest query tile down, so
   // the heaviest tiles (most keys under the causal mask) of every row come
@@ -177,12 +201,13 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanArgs a) {
     return;
   }
   // General case: one block scan per (level, chunk of rows).
-  base = 0;
+  int base = 0;
   for (int lev = nlev - 1; lev >= 0; --lev) {
     for (int b0 = 0; b0 < a.B; b0 += kPlanThreads) {
       const int b = b0 + tid;
-      int nd, np, q0, kl, tot;
-      row_work(a, b, nd, np, q0, kl);
+      bool dec;
+      int np, q0, kl, tot;
+      row_work(a, b, dec, np, q0, kl);
       const int f = np > lev ? 1 : 0;
       const int incl = block_scan_1024(f, scan_lds, tot);
       if (f) pl.plist[base + incl - 1] = b * pl.ntq + lev;
@@ -206,17 +231,19 @@ int device_slots(int per_cu) {
   return g_cus[dev] * per_cu;
 }
 
-int launch_plan(const AttnParams& P, const Plan& plan, bool paged, hipStream_t stream) {
+int launch_plan(const AttnParams& P, const Plan& plan, bool paged, int decode_waves, hipStream_t stream) {
   PlanArgs a;
   a.cu_q = P.cu_q;
   a.cu_k = P.cu_k;
-  a.bt = P.bt;
-  a.bt_stride = P.bt_stride;
-  a.NB = P.NB;
-  a.bs = P.bs > 0 ? P.bs : 1;
   a.B = P.B;
   a.T = P.T;
   a.paged = paged ? 1 : 0;
+  a.Hq = P.Hq;
+  a.Hkv = P.Hkv;
+  a.waves = decode_waves;
+  a.out = (uint16_t*)P.out;
+  a.out_ts = P.out_ts;
+  a.out_hs = P.out_hs;
   a.plan = plan;
   hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(1024), 0, stream, a);
   return check_launch("plan");
