@@ -14,6 +14,7 @@ static int validate_common(const AttnParams& P, const char* who) {
   NVS_REQUIRE(P.Hq > 0 && P.Hkv > 0 && P.Hq % P.Hkv == 0, NVS_ERR_INVALID,
               "%s: num_heads (%d) must be a positive multiple of num_kv_heads (%d)", who, P.Hq,
               P.Hkv);
+  NVS_REQUIRE(P.Hkv <= 256, NVS_ERR_UNSUPPORTED, "%s: at most 256 kv heads, got %d", who, P.Hkv);
   NVS_REQUIRE(P.Hq / P.Hkv <= 16, NVS_ERR_UNSUPPORTED,
               "%s: at most 16 query heads per kv head, got %d", who, P.Hq / P.Hkv);
   NVS_REQUIRE(P.max_seqlen_q >= 0 && P.max_seqlen_k >= 0, NVS_ERR_INVALID,
@@ -61,8 +62,11 @@ static Plan make_plan(void* ws, const AttnParams& P) {
   return plan_at(ws, P.B, decode_wave_cap(P.B, P.max_seqlen_k, P.Hkv), prefill_tiles(P.max_seqlen_q, pbm), pbm);
 }
 
-int decode_launch_waves(const Plan& plan) {
-  return std::min(plan.max_waves, device_slots(4 * kDecodeWavesPerEU));
+// Whole groups of Hkv waves: the workspace bound and the device's resident
+// wave slots, whichever is smaller (at least one group).
+int decode_launch_waves(const Plan& plan, int Hkv) {
+  const int w = std::min(plan.max_waves, device_slots(4 * kDecodeWavesPerEU));
+  return std::max(Hkv, w / Hkv * Hkv);
 }
 }  // namespace nvs
 
@@ -125,16 +129,15 @@ extern "C" int nvs_paged_attention(const void* q, int64_t q_tok_stride, int64_t 
               NVS_ERR_INVALID,
               "paged_attention: block_tables rows (%lld) too short for max_seqlen_k %d",
               (long long)bt_stride, max_seqlen_k);
-  NVS_REQUIRE((int64_t)num_seqs * num_kv_heads * (((int64_t)max_seqlen_k + kDecodeTile - 1) / kDecodeTile) <
-                  (1ll << 31),
-              NVS_ERR_UNSUPPORTED, "paged_attention: batch too large for one call (decode units exceed 2^31)");
+  NVS_REQUIRE((int64_t)num_seqs * (((int64_t)max_seqlen_k + kDecodeTile - 1) / kDecodeTile) < (1ll << 31),
+              NVS_ERR_UNSUPPORTED, "paged_attention: batch too large for one call (decode tiles exceed 2^31)");
   if (max_seqlen_q <= 0) return NVS_OK;
   rc = check_workspace(P, "paged_attention");
   if (rc != NVS_OK) return rc;
   hipStream_t s = (hipStream_t)stream;
   const Plan plan = make_plan(workspace, P);
   char* partials = (char*)workspace + align256(plan_bytes(num_seqs, plan.max_waves, plan.ntq));
-  const int waves = decode_launch_waves(plan);
+  const int waves = decode_launch_waves(plan, num_kv_heads);
   rc = launch_plan(P, plan, /*paged=*/true, waves, s);
   if (rc != NVS_OK) return rc;
   rc = launch_decode(P, plan, waves, partials, s);

@@ -71,12 +71,13 @@ __device__ __forceinline__ bf16x8 codes8_to_bf16x8(uint32_t lo, uint32_t hi) {
 // empty on ragged batches).
 //   decode rows:  one DecodeRow per q_len == 1 row of a paged call with at
 //                 least one visible key (the plan zeroes the others).  Decode
-//                 work is counted in units, one per (row, kv head, 32-key
-//                 tile), ordered row-major, then kv head, then tile.  A
-//                 unit range [s_w, e_w) with s_w = floor(w U / W) goes to
-//                 decode wave w of W (stream-K: every wave gets the same
-//                 number of units and streams across row boundaries).
-//   wave starts:  the (row, kv head, tile) of each wave's first unit.
+//                 work is counted in 32-key tiles of the rows, in row order
+//                 (T in all).  Waves form Kw groups of Hkv, one wave per kv
+//                 head; group k takes tiles [s_k, s_{k+1}), s_k = floor(k T /
+//                 Kw), for its Hkv heads (stream-K: every wave gets the same
+//                 work and streams across row boundaries, and the Hkv waves of
+//                 a group read the same token rows side by side).
+//   group starts: the (row, tile) of each group's first tile.
 //   prefill list: b * ntq + qt, one entry per (q_len > 1 row, tile of
 //                 prefill_positions(g) query positions), every row's tiles in
 //                 descending qt (heaviest first).
@@ -97,20 +98,20 @@ struct DecodeRow {
   int b;       // sequence (row of cu_seqlens)
   int q0;      // query / output row
   int K;       // visible keys (k_len)
-  int n;       // 32-key tiles, ceil(K / 32); 0 for a row without keys
-  int prefix;  // first unit of the row: sum over earlier rows of Hkv * n
+  int n;       // 32-key tiles, ceil(K / 32) >= 1
+  int prefix;  // first tile of the row: sum of n over earlier rows
   int pad[3];
 };
 static_assert(sizeof(DecodeRow) == 32, "decode rows are 32 bytes");
 
 struct WaveStart {
-  int row, h, t, pad;  // decode row index, kv head and tile of the wave's first unit
+  int row, t, pad[2];  // decode row index and tile of a wave group's first tile
 };
 
 struct PlanHeader {
   int n_rows;           // decode rows
-  int n_units;          // decode units U
-  int n_waves;          // decode waves W with work (W <= U)
+  int n_units;          // decode tiles T
+  int n_groups;         // decode wave groups Kw with work (Kw <= T); Kw * Hkv waves
   int n_prefill;        // prefill list entries
   int prefill_next[8];  // per-XCD work counters of the prefill kernel (zeroed by the plan)
   int pad[52];          // keeps the lists 256-byte aligned
@@ -122,20 +123,25 @@ struct Plan {
   DecodeRow* rows;
   WaveStart* starts;
   int* plist;
-  int max_waves;  // decode waves the call may use (bound of the start list and the partials)
+  int max_waves;  // decode waves the call may use (bounds the start list and the partials)
   int ntq;        // prefill query tiles per sequence (list stride)
   int pbm;        // query positions per prefill tile
 };
 
 inline int64_t align256(int64_t x) { return (x + 255) & ~(int64_t)255; }
 
-// Decode waves a call may use: at most kDecodeMaxWaves, and no more than the
-// units there can be (B rows x Hkv heads x ceil(max_seqlen_k / 32) tiles)
-// allow at kDecodeMinUnits each.
+// Decode waves a call may use: Hkv per group, at most kDecodeMaxWaves in
+// all, and no more groups than the tiles there can be (B rows x
+// ceil(max_seqlen_k / 32)) allow at kDecodeMinUnits each, rounded up to a
+// multiple of 8 groups (one per XCD of a launch round).
 inline int decode_wave_cap(int B, int max_seqlen_k, int Hkv) {
-  const int64_t units = (int64_t)B * (Hkv > 0 ? Hkv : 1) * ((max_seqlen_k + kDecodeTile - 1) / kDecodeTile);
-  const int64_t w = (units + kDecodeMinUnits - 1) / kDecodeMinUnits;
-  return (int)(w < 1 ? 1 : (w > kDecodeMaxWaves ? kDecodeMaxWaves : w));
+  const int hk = Hkv > 0 ? Hkv : 1;
+  const int64_t tiles = (int64_t)B * ((max_seqlen_k + kDecodeTile - 1) / kDecodeTile);
+  int64_t groups = (tiles + kDecodeMinUnits - 1) / kDecodeMinUnits;
+  groups = (groups + 7) / 8 * 8;
+  const int64_t gmax = kDecodeMaxWaves / hk > 0 ? kDecodeMaxWaves / hk : 1;
+  groups = groups < 1 ? 1 : (groups > gmax ? gmax : groups);
+  return (int)(groups * hk);
 }
 
 // Bytes of the plan for a batch; it sits at the start of the workspace.
@@ -201,7 +207,7 @@ int64_t attention_workspace_bytes(int num_seqs, int max_seqlen_q, int max_seqlen
                                   int num_kv_heads);
 // Decode waves a paged call launches: its workspace bound and the device's
 // resident wave slots, whichever is smaller.
-int decode_launch_waves(const Plan& plan);
+int decode_launch_waves(const Plan& plan, int Hkv);
 int launch_plan(const AttnParams& P, const Plan& plan, bool paged, int decode_waves, hipStream_t stream);
 int launch_decode(const AttnParams& P, const Plan& plan, int waves, void* partials, hipStream_t stream);
 int launch_prefill(const AttnParams& P, const Plan& plan, hipStream_t stream);

@@ -85,7 +85,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanArgs a) {
     if (b0 == 0) np0 = np;
     deepest = max(deepest, np);
     const int n = dec && kl > 0 ? (kl + kDecodeTile - 1) / kDecodeTile : 0;
-    const int u = a.Hkv * n;
+    const int u = n;
     const int ir = block_scan_1024(n > 0 ? 1 : 0, scan_lds, tot_r);
     const int iu = block_scan_1024(u, scan_lds, tot_u);
     if (n > 0) {
@@ -106,44 +106,44 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanArgs a) {
     nrows += tot_r;
     units += tot_u;
   }
-  const int nwaves = units > 0 ? (int)min((int64_t)a.waves, max((int64_t)1, (int64_t)units / kDecodeMinUnits)) : 0;
+  // Wave groups: Kw groups of Hkv waves (one per kv head), at most the
+  // launched waves and at least kDecodeMinUnits tiles per group.
+  const int ngroups = units > 0 ? (int)min((int64_t)(a.waves / a.Hkv), max((int64_t)1, (int64_t)units / kDecodeMinUnits)) : 0;
   if (tid == 0) {
     pl.hdr->n_rows = nrows;
     pl.hdr->n_units = units;
-    pl.hdr->n_waves = nwaves;
+    pl.hdr->n_groups = ngroups;
   }
 
-  // ---- wave starts: wave w begins at unit s_w = floor(w U / W), inside the
-  // first row whose inclusive unit prefix exceeds s_w.
-  if (nwaves > 0) {
+  // ---- group starts: group k begins at tile s_k = floor(k T / Kw), inside
+  // the first row whose inclusive tile prefix exceeds s_k.
+  if (ngroups > 0) {
     int rbase = 0, ubase = 0;
     for (int b0 = 0; b0 < a.B; b0 += kPlanThreads) {
       bool dec;
       int np, q0, kl, tot_r, tot_u;
       row_work(a, b0 + tid, dec, np, q0, kl);
       const int n = dec && kl > 0 ? (kl + kDecodeTile - 1) / kDecodeTile : 0;
-      const int u = a.Hkv * n;
+      const int u = n;
       const int ir = block_scan_1024(n > 0 ? 1 : 0, scan_lds, tot_r);
       const int iu = block_scan_1024(u, scan_lds, tot_u);
       row_incl[tid] = ubase + iu;
       row_idx[tid] = rbase + ir - 1;
       row_n[tid] = n;
       __syncthreads();
-      for (int wv = tid; wv < nwaves; wv += kPlanThreads) {
-        const int sw = (int)((int64_t)wv * units / nwaves);
+      for (int k = tid; k < ngroups; k += kPlanThreads) {
+        const int sw = (int)((int64_t)k * units / ngroups);
         if (sw < ubase || sw >= ubase + tot_u) continue;
         int lo = 0, hi = kPlanThreads - 1;  // first r with row_incl[r] > sw
         while (lo < hi) {
           const int mid = (lo + hi) >> 1;
           if (row_incl[mid] > sw) hi = mid; else lo = mid + 1;
         }
-        const int rn = row_n[lo], rel = sw - (row_incl[lo] - a.Hkv * rn);
         WaveStart st;
         st.row = row_idx[lo];
-        st.h = rel / rn;
-        st.t = rel - st.h * rn;
-        st.pad = 0;
-        pl.starts[wv] = st;
+        st.t = sw - (row_incl[lo] - row_n[lo]);
+        st.pad[0] = st.pad[1] = 0;
+        pl.starts[k] = st;
       }
       rbase += tot_r;
       ubase += tot_u;

@@ -178,23 +178,25 @@ def test_c_abi_validates_before_launch():
 def test_workspace_bytes():
     """Plan (256-byte header, 32-byte decode rows, 16-byte decode wave
     starts, prefill list, each 256-aligned) followed by the decode partials:
-    two slots of g x (128 + 2) floats per decode wave.  Decode waves: at most
-    2048, and at most one per 4 units (kv head x 32-key tile) the batch can
-    hold."""
+    two slots of g x (128 + 2) floats per decode wave.  Decode waves come in
+    groups of Hkv: at most 2048 waves, and at most one group per 4 32-key
+    tiles the batch can hold, rounded up to a multiple of 8 groups."""
     lib = _lib.load()
     a256 = lambda x: (x + 255) // 256 * 256
 
     def expect(B, max_q, max_k, Hq, Hkv):
         g = Hq // Hkv if Hkv > 0 and Hq % Hkv == 0 else 1
-        units = B * max(Hkv, 1) * ((max_k + 31) // 32)
-        waves = min(2048, max(1, (units + 3) // 4))
+        hk = max(Hkv, 1)
+        tiles = B * ((max_k + 31) // 32)
+        groups = ((tiles + 3) // 4 + 7) // 8 * 8
+        waves = hk * min(2048 // hk, max(1, groups))
         gg = Hq // Hkv if Hkv > 0 and Hq % Hkv == 0 else 0
         pbm = 32 * (8 // min(gg, 8)) if gg > 0 else 32
         ntq = max(1, (max_q + pbm - 1) // pbm)
         plan = 256 + a256(B * 32) + a256(waves * 16) + a256(B * ntq * 4)
         return a256(plan) + waves * 2 * g * 130 * 4
 
-    # 64 decode rows, max_k 256: 64 x 8 x 8 units -> 1024 waves
+    # 64 decode rows, max_k 256: 512 tiles -> 128 groups of 8 waves
     assert lib.nvs_attention_workspace_bytes(64, 1, 256, 32, 8, 128, 256) == expect(64, 1, 256, 32, 8)
     assert expect(64, 1, 256, 32, 8) == a256(256 + a256(64 * 32) + a256(1024 * 16) + a256(64 * 4)) + 1024 * 2 * 4 * 130 * 4
     # max_k 8192: the 2048-wave cap
