@@ -48,24 +48,22 @@ static int group_of(int num_heads, int num_kv_heads) {
   return (num_kv_heads > 0 && num_heads % num_kv_heads == 0) ? num_heads / num_kv_heads : 1;
 }
 
+// Workspace: the prefill plan, then the decode partials (256-byte aligned).
 int64_t attention_workspace_bytes(int num_seqs, int max_seqlen_q, int max_seqlen_k, int num_heads,
                                   int num_kv_heads) {
   if (num_seqs <= 0 || num_heads <= 0) return 0;
   const int waves = decode_wave_cap(num_seqs, max_seqlen_k, num_kv_heads);
   const int ntq = prefill_tiles(max_seqlen_q, prefill_pbm(num_heads, num_kv_heads));
-  return align256(plan_bytes(num_seqs, waves, ntq)) +
-         decode_workspace_bytes(waves, group_of(num_heads, num_kv_heads));
+  return align256(plan_bytes(num_seqs, ntq)) + decode_workspace_bytes(waves, group_of(num_heads, num_kv_heads));
 }
 
 static Plan make_plan(void* ws, const AttnParams& P) {
   const int pbm = prefill_pbm(P.Hq, P.Hkv);
-  return plan_at(ws, P.B, decode_wave_cap(P.B, P.max_seqlen_k, P.Hkv), prefill_tiles(P.max_seqlen_q, pbm), pbm);
+  return plan_at(ws, prefill_tiles(P.max_seqlen_q, pbm), pbm);
 }
 
-// Whole groups of Hkv waves: the workspace bound and the device's resident
-// wave slots, whichever is smaller (at least one group).
-int decode_launch_waves(const Plan& plan, int Hkv) {
-  const int w = std::min(plan.max_waves, device_slots(4 * kDecodeWavesPerEU));
+int decode_launch_waves(int max_waves, int Hkv) {
+  const int w = std::min(max_waves, device_slots(4 * kDecodeWavesPerEU));
   return std::max(Hkv, w / Hkv * Hkv);
 }
 }  // namespace nvs
@@ -136,12 +134,12 @@ extern "C" int nvs_paged_attention(const void* q, int64_t q_tok_stride, int64_t 
   if (rc != NVS_OK) return rc;
   hipStream_t s = (hipStream_t)stream;
   const Plan plan = make_plan(workspace, P);
-  char* partials = (char*)workspace + align256(plan_bytes(num_seqs, plan.max_waves, plan.ntq));
-  const int waves = decode_launch_waves(plan, num_kv_heads);
-  rc = launch_plan(P, plan, /*paged=*/true, waves, s);
+  char* partials = (char*)workspace + align256(plan_bytes(num_seqs, plan.ntq));
+  const int max_waves = decode_wave_cap(num_seqs, max_seqlen_k, num_kv_heads);
+  rc = launch_decode(P, max_waves, decode_launch_waves(max_waves, num_kv_heads), partials, s);
+  if (rc != NVS_OK || max_seqlen_q == 1) return rc;  // no prefill rows: no plan
+  rc = launch_plan(P, plan, /*paged=*/true, s);
   if (rc != NVS_OK) return rc;
-  rc = launch_decode(P, plan, waves, partials, s);
-  if (rc != NVS_OK || max_seqlen_q == 1) return rc;
   return launch_prefill(P, plan, s);
 }
 
@@ -179,7 +177,7 @@ extern "C" int nvs_varlen_attention(const void* q, int64_t q_tok_stride, int64_t
   if (rc != NVS_OK) return rc;
   hipStream_t s = (hipStream_t)stream;
   const Plan plan = make_plan(workspace, P);
-  rc = launch_plan(P, plan, /*paged=*/false, 0, s);
+  rc = launch_plan(P, plan, /*paged=*/false, s);
   if (rc != NVS_OK) return rc;
   return launch_prefill(P, plan, s);
 }

@@ -64,20 +64,19 @@ __device__ __forceinline__ bf16x8 codes8_to_bf16x8(uint32_t lo, uint32_t hi) {
 }
 
 // ---------------------------------------------------------------------------
-// Work plan.  A one-work-group planning kernel turns cu_seqlens into compact
-// work lists in the workspace, on the device, so the attention kernels
-// launch a fixed persistent grid and never dispatch empty work-groups (each
-// costs the dispatcher several nanoseconds; an upper-bound grid is mostly
-// empty on ragged batches).
-//   decode rows:  one DecodeRow per q_len == 1 row of a paged call with at
-//                 least one visible key (the plan zeroes the others).  Decode
-//                 work is counted in 32-key tiles of the rows, in row order
-//                 (T in all).  Waves form Kw groups of Hkv, one wave per kv
-//                 head; group k takes tiles [s_k, s_{k+1}), s_k = floor(k T /
-//                 Kw), for its Hkv heads (stream-K: every wave gets the same
-//                 work and streams across row boundaries, and the Hkv waves of
-//                 a group read the same token rows side by side).
-//   group starts: the (row, tile) of each group's first tile.
+// Decode scheduling (paged calls): decode work is counted in 32-key tiles of
+// the decode rows (q_len == 1 rows with a visible key), in row order, T in
+// all.  Waves form groups of Hkv, one wave per kv head; of the Kw groups with
+// work, group k takes tiles [floor(k T / Kw), floor((k + 1) T / Kw)) for its
+// Hkv heads (stream-K: every wave gets the same work and streams across row
+// boundaries).  The decode waves derive all of this from cu_seqlens
+// themselves; rows split across groups leave partials in the workspace.
+//
+// Prefill work plan: a one-work-group planning kernel turns cu_seqlens into
+// the prefill list in the workspace, on the device, so the prefill kernel
+// launches a fixed persistent grid and never dispatches empty work-groups
+// (each costs the dispatcher several nanoseconds; an upper-bound grid is
+// mostly empty on ragged batches).
 //   prefill list: b * ntq + qt, one entry per (q_len > 1 row, tile of
 //                 prefill_positions(g) query positions), every row's tiles in
 //                 descending qt (heaviest first).
@@ -94,38 +93,18 @@ __host__ __device__ inline int prefill_positions(int g) {
 }
 __host__ __device__ inline int prefill_head_groups(int g) { return (g + kPrefillWaves - 1) / kPrefillWaves; }
 
-struct DecodeRow {
-  int b;       // sequence (row of cu_seqlens)
-  int q0;      // query / output row
-  int K;       // visible keys (k_len)
-  int n;       // 32-key tiles, ceil(K / 32) >= 1
-  int prefix;  // first tile of the row: sum of n over earlier rows
-  int pad[3];
-};
-static_assert(sizeof(DecodeRow) == 32, "decode rows are 32 bytes");
-
-struct WaveStart {
-  int row, t, pad[2];  // decode row index and tile of a wave group's first tile
-};
-
 struct PlanHeader {
-  int n_rows;           // decode rows
-  int n_units;          // decode tiles T
-  int n_groups;         // decode wave groups Kw with work (Kw <= T); Kw * Hkv waves
   int n_prefill;        // prefill list entries
   int prefill_next[8];  // per-XCD work counters of the prefill kernel (zeroed by the plan)
-  int pad[52];          // keeps the lists 256-byte aligned
+  int pad[55];          // keeps the list 256-byte aligned
 };
 static_assert(sizeof(PlanHeader) == 256, "plan header is one 256-byte line");
 
 struct Plan {
   PlanHeader* hdr;
-  DecodeRow* rows;
-  WaveStart* starts;
   int* plist;
-  int max_waves;  // decode waves the call may use (bounds the start list and the partials)
-  int ntq;        // prefill query tiles per sequence (list stride)
-  int pbm;        // query positions per prefill tile
+  int ntq;  // prefill query tiles per sequence (list stride)
+  int pbm;  // query positions per prefill tile
 };
 
 inline int64_t align256(int64_t x) { return (x + 255) & ~(int64_t)255; }
@@ -145,22 +124,14 @@ inline int decode_wave_cap(int B, int max_seqlen_k, int Hkv) {
 }
 
 // Bytes of the plan for a batch; it sits at the start of the workspace.
-inline int64_t plan_bytes(int B, int max_waves, int ntq) {
-  return (int64_t)sizeof(PlanHeader) + align256((int64_t)B * sizeof(DecodeRow)) +
-         align256((int64_t)max_waves * sizeof(WaveStart)) + align256((int64_t)B * ntq * 4);
+inline int64_t plan_bytes(int B, int ntq) {
+  return (int64_t)sizeof(PlanHeader) + align256((int64_t)B * ntq * 4);
 }
 
-inline Plan plan_at(void* ws, int B, int max_waves, int ntq, int pbm) {
+inline Plan plan_at(void* ws, int ntq, int pbm) {
   Plan p;
-  char* c = (char*)ws;
-  p.hdr = (PlanHeader*)c;
-  c += sizeof(PlanHeader);
-  p.rows = (DecodeRow*)c;
-  c += align256((int64_t)B * sizeof(DecodeRow));
-  p.starts = (WaveStart*)c;
-  c += align256((int64_t)max_waves * sizeof(WaveStart));
-  p.plist = (int*)c;
-  p.max_waves = max_waves;
+  p.hdr = (PlanHeader*)ws;
+  p.plist = (int*)((char*)ws + sizeof(PlanHeader));
   p.ntq = ntq;
   p.pbm = pbm;
   return p;
@@ -205,11 +176,12 @@ struct AttnParams {
 int64_t decode_workspace_bytes(int max_waves, int group);
 int64_t attention_workspace_bytes(int num_seqs, int max_seqlen_q, int max_seqlen_k, int num_heads,
                                   int num_kv_heads);
-// Decode waves a paged call launches: its workspace bound and the device's
-// resident wave slots, whichever is smaller.
-int decode_launch_waves(const Plan& plan, int Hkv);
-int launch_plan(const AttnParams& P, const Plan& plan, bool paged, int decode_waves, hipStream_t stream);
-int launch_decode(const AttnParams& P, const Plan& plan, int waves, void* partials, hipStream_t stream);
+// Decode waves a paged call launches: whole groups of Hkv, its workspace
+// bound (max_waves) and the device's resident wave slots, whichever is
+// smaller.
+int decode_launch_waves(int max_waves, int Hkv);
+int launch_plan(const AttnParams& P, const Plan& plan, bool paged, hipStream_t stream);
+int launch_decode(const AttnParams& P, int max_waves, int waves, void* partials, hipStream_t stream);
 int launch_prefill(const AttnParams& P, const Plan& plan, hipStream_t stream);
 
 }  // namespace nvs

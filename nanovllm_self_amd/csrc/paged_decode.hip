@@ -47,7 +47,10 @@ struct DecodeArgs {
   float scale_log2;
   float* ws_o;   // [max_waves, 2 slots, g, 128]
   float* ws_ml;  // [max_waves, 2 slots, g, 2]
-  PlanHeader* hdr;
+  const int32_t* cu_q;
+  const int32_t* cu_k;
+  int B;
+  int64_t T;  // query / output rows
   uint16_t* out;
   int64_t out_ts, out_hs;
 };
@@ -301,27 +304,156 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// ---------------------------------------------------------------------------
+// Scheduling, on the device and without a planning launch: decode work is
+// counted in 32-key tiles of the decode rows (q_len == 1 rows with at least
+// one visible key), in row order, T in all.  Every wave derives T, the group
+// count Kw and its group's first tile from cu_seqlens itself, scanning the
+// batch 64 rows at a time (one row per lane).
+// ---------------------------------------------------------------------------
+
+// Row b of the batch: whether it is a decode row (q_len == 1; malformed rows
+// are skipped), its output row and key count.
+struct RowInfo {
+  bool dec;
+  int q0, K;
+};
+
+__device__ __forceinline__ RowInfo row_info(const DecodeArgs& a, const int32_t* __restrict__ cu_q,
+                                            const int32_t* __restrict__ cu_k, int b) {
+  RowInfo r;
+  r.q0 = cu_q[b];
+  const int q1 = cu_q[b + 1];
+  r.K = cu_k[b + 1] - cu_k[b];
+  r.dec = q1 - r.q0 == 1 && r.q0 >= 0 && (int64_t)q1 <= a.T;
+  return r;
+}
+
+__device__ __forceinline__ int row_tiles(const RowInfo& r) {
+  return r.dec && r.K > 0 ? (r.K + kDecodeTile - 1) / kDecodeTile : 0;
+}
+
+// 64 rows of the batch: lane l holds row c0 + l's tile count (0 unless it is
+// a decode row with a visible key).
+struct Chunk {
+  int c0;
+  int n;
+};
+
+__device__ __forceinline__ Chunk load_chunk(const DecodeArgs& a, const int32_t* __restrict__ cu_q,
+                                            const int32_t* __restrict__ cu_k, int c0) {
+  Chunk ch;
+  ch.c0 = c0;
+  const int b = c0 + (int)threadIdx.x;
+  ch.n = b < a.B ? row_tiles(row_info(a, cu_q, cu_k, b)) : 0;
+  return ch;
+}
+
+// Wave sum; every lane holds it after the butterfly, and readfirstlane tells
+// the compiler it is wave-uniform (else everything derived from it, down to
+// the tile cursors, would be treated as divergent and kept in VGPRs).
+__device__ __forceinline__ int wave_sum_i(int v) {
+#pragma unroll
+  for (int s = 32; s >= 1; s >>= 1) v += __shfl_xor(v, s, 64);
+  return __builtin_amdgcn_readfirstlane(v);
+}
+
+__device__ __forceinline__ int wave_incl_scan(int v) {
+  const int lane = threadIdx.x;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int t = __shfl_up(v, off, 64);
+    if (lane >= off) v += t;
+  }
+  return v;
+}
+
+// Total decode tiles of the batch.
+__device__ __forceinline__ int decode_tiles(const DecodeArgs& a, const int32_t* __restrict__ cu_q,
+                                            const int32_t* __restrict__ cu_k) {
+  int tot = 0;
+  for (int c0 = 0; c0 < a.B; c0 += 64) tot += wave_sum_i(load_chunk(a, cu_q, cu_k, c0).n);
+  return tot;
+}
+
 // Position of a decode wave in its tile stream: a decode row and a tile.
 // All members are wave-uniform (scalar registers).
 struct Cursor {
-  int row;          // decode row index
-  int b, q0, K, n;  // that row (DecodeRow)
+  int b, q0, K, n;  // the row
   int t;            // tile
+  int lb, koff;     // its logical block and key offset in the block (kept
+                    // incrementally: a division by block_size would be VALU)
 };
 
-__device__ __forceinline__ void set_row(Cursor& c, const DecodeRow& r, int row) {
-  c.row = row;
-  c.b = r.b;
-  c.q0 = r.q0;
-  c.K = r.K;
-  c.n = r.n;
+// Cursor c at lane li of chunk ch; the row's output row and key count are
+// scalar loads.
+__device__ __forceinline__ void set_row(const DecodeArgs& a, const int32_t* __restrict__ cu_q,
+                                        const int32_t* __restrict__ cu_k, Cursor& c, const Chunk& ch, int li) {
+  c.b = ch.c0 + li;
+  c.n = __builtin_amdgcn_readlane(ch.n, li);
+  c.q0 = cu_q[c.b];
+  c.K = cu_k[c.b + 1] - cu_k[c.b];
+}
+
+// The decode row and tile of tile index s (< T): the chunk holding the row
+// and a cursor at it.  Also returns the row's first tile index.
+__device__ __forceinline__ void locate_tile(const DecodeArgs& a, const int32_t* __restrict__ cu_q,
+                                            const int32_t* __restrict__ cu_k, int s, Chunk& ch, Cursor& c,
+                                            int& first) {
+  int base = 0;
+  for (int c0 = 0; c0 < a.B; c0 += 64) {
+    ch = load_chunk(a, cu_q, cu_k, c0);
+    const int incl = base + wave_incl_scan(ch.n);
+    const uint64_t m = __ballot(incl > s);
+    if (m) {
+      const int li = __builtin_amdgcn_readfirstlane(__builtin_ctzll(m));
+      set_row(a, cu_q, cu_k, c, ch, li);
+      first = __builtin_amdgcn_readlane(incl, li) - c.n;
+      c.t = s - first;
+      // The search result is wave-uniform; say so, so the cursor stays in
+      // scalar registers and its loads are scalar loads.
+      c.b = __builtin_amdgcn_readfirstlane(c.b);
+      c.q0 = __builtin_amdgcn_readfirstlane(c.q0);
+      c.K = __builtin_amdgcn_readfirstlane(c.K);
+      c.n = __builtin_amdgcn_readfirstlane(c.n);
+      c.t = __builtin_amdgcn_readfirstlane(c.t);
+      first = __builtin_amdgcn_readfirstlane(first);
+      c.lb = __builtin_amdgcn_readfirstlane((c.t * kDecodeTile) / a.bs);
+      c.koff = c.t * kDecodeTile - c.lb * a.bs;
+      return;
+    }
+    base = __builtin_amdgcn_readlane(incl, 63);
+  }
+  // Unreachable for s < T; an in-bounds cursor at row 0 keeps every access valid.
+  ch = load_chunk(a, cu_q, cu_k, 0);
+  set_row(a, cu_q, cu_k, c, ch, 0);
+  c.t = c.lb = c.koff = 0;
+  c.n = 1;
+  first = 0;
+}
+
+// Moves cursor x to the next decode row with keys (scalar loads; in a pure
+// decode batch that is the next row).  Past the last row the cursor stays.
+__device__ __forceinline__ void next_row(const DecodeArgs& a, const int32_t* __restrict__ cu_q,
+                                         const int32_t* __restrict__ cu_k, Cursor& x) {
+  for (int b = x.b + 1; b < a.B; ++b) {
+    const RowInfo r = row_info(a, cu_q, cu_k, b);
+    const int n = row_tiles(r);
+    if (n > 0) {
+      x.b = b;
+      x.q0 = r.q0;
+      x.K = r.K;
+      x.n = n;
+      break;
+    }
+  }
+  x.t = x.lb = x.koff = 0;
 }
 
 // Block id of cursor c's tile (-1 where the table has none or it is outside
 // the pool); a 32-key tile never spans two blocks (block_size % 64 == 0).
 __device__ __forceinline__ int tile_block(const DecodeArgs& a, const int32_t* __restrict__ bt, const Cursor& c) {
-  const int lb = (c.t * kDecodeTile) / a.bs;
-  const int blk = lb < a.bt_stride ? bt[(int64_t)c.b * a.bt_stride + lb] : -1;
+  const int blk = c.lb < a.bt_stride ? bt[(int64_t)c.b * a.bt_stride + c.lb] : -1;
   return (blk >= 0 && blk < a.NB) ? blk : -1;
 }
 
@@ -370,18 +502,19 @@ __device__ __forceinline__ void finish_segment(const DecodeArgs& a, const Cursor
 }
 
 // One decode wave (kv head h of group k): the tiles [floor(k T / Kw),
-// floor((k + 1) T / Kw)) of the plan, streamed one by one.  Cursor c is the tile being computed, n1 the
-// next one (its loads are in flight during c's compute) and n2 the one after
-// (its block id is fetched during c's compute).  Loads are issued
-// unconditionally (past the wave's last unit the cursors stop advancing, so
-// the surplus loads re-read the last tile) and the two-tile ring is unrolled
-// so every buffer index is a compile-time constant.  Row, block-table and
-// start records are read through restrict-qualified pointers, so they are
-// scalar loads whose waits never wait for the wave's vector loads.
+// floor((k + 1) T / Kw)) of the batch, streamed one by one.  Cursor c is the
+// tile being computed, n1 the next one (its loads are in flight during c's
+// compute) and n2 the one after (its block id is fetched during c's
+// compute).  Loads are issued unconditionally (past the wave's last tile the
+// cursors stop advancing, so the surplus loads re-read the last tile) and the
+// two-tile ring is unrolled so every buffer index is a compile-time
+// constant.  The block table is read through a restrict-qualified pointer, so
+// its entries are scalar loads whose waits never wait for the wave's vector
+// loads.
 template <int KV>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kDecodeWavesPerEU)))
-void paged_decode_kernel(DecodeArgs a, const DecodeRow* __restrict__ rows, const WaveStart* __restrict__ starts,
-                         const int32_t* __restrict__ bt) {
+void paged_decode_kernel(DecodeArgs a, const int32_t* __restrict__ bt, const int32_t* __restrict__ cu_q,
+                         const int32_t* __restrict__ cu_k) {
   // Launch index -> (kv head h, group k) with the group fastest: work-group
   // i runs on XCD i % 8, so with a multiple of 8 launched groups the Hkv waves
   // of a group share an XCD and their slices of each 2 KiB token row reach
@@ -389,30 +522,30 @@ void paged_decode_kernel(DecodeArgs a, const DecodeRow* __restrict__ rows, const
   const int G = gridDim.x / a.Hkv;
   const int h = blockIdx.x / G, k = blockIdx.x - h * G;
   const int w = k * a.Hkv + h;  // partial slot index
-  const int Kw = a.hdr->n_groups;
+  const int lane = threadIdx.x;
+
+  const int T = decode_tiles(a, cu_q, cu_k);
+  const int Kw = T > 0 ? min(G, max(1, T / kDecodeMinUnits)) : 0;
   if (k >= Kw) return;
-  const int T = a.hdr->n_units;
-  const int nrows = a.hdr->n_rows;
   const int s0 = (int)((int64_t)k * T / Kw);
   const int left = (int)((int64_t)(k + 1) * T / Kw) - s0;  // >= 1 (Kw <= T)
 
-  const int lane = threadIdx.x;
   const int col = lane & 15, grp = lane >> 4;
   const LaneOffsets lo = lane_offsets<KV>(a.Hkv, col, grp);
 
-  // Cursors.  nxt holds the row after n2's row, prefetched.
+  // Cursors.
   Cursor c;
   {
-    const WaveStart st = starts[k];
-    set_row(c, rows[st.row], st.row);
-    c.t = st.t;
+    Chunk ch;
+    int first;
+    locate_tile(a, cu_q, cu_k, s0, ch, c, first);
   }
-  DecodeRow nxt = rows[min(c.row + 1, nrows - 1)];
   auto advance = [&](Cursor& x) {
     if (++x.t == x.n) {
-      x.t = 0;
-      set_row(x, nxt, x.row + 1);
-      nxt = rows[min(x.row + 1, nrows - 1)];
+      next_row(a, cu_q, cu_k, x);
+    } else if ((x.koff += kDecodeTile) == a.bs) {
+      x.koff = 0;
+      ++x.lb;
     }
   };
   Cursor n1 = c;
@@ -430,12 +563,12 @@ void paged_decode_kernel(DecodeArgs a, const DecodeRow* __restrict__ rows, const
   int slot = 0;      // partial slot of the current segment (0: the wave's first)
 
   DecodeTile<KV> r0, r1;
-  decode_load<KV>(r0, a, lo, tile_block(a, bt, c), c.t * kDecodeTile % a.bs, h);
+  decode_load<KV>(r0, a, lo, tile_block(a, bt, c), c.koff, h);
   int blk1 = tile_block(a, bt, n1);
 
   // Tile i (cursor c) from ring slot cur; the loads of tile i + 1 go to nxt_t.
   auto step = [&](DecodeTile<KV>& cur, DecodeTile<KV>& nxt_t, int i) {
-    decode_load<KV>(nxt_t, a, lo, blk1, n1.t * kDecodeTile % a.bs, h);
+    decode_load<KV>(nxt_t, a, lo, blk1, n1.koff, h);
     const int blk2 = tile_block(a, bt, n2);
     __builtin_amdgcn_sched_barrier(0);
     if (!cur.has) zero_tile(cur);
@@ -471,7 +604,8 @@ void paged_decode_kernel(DecodeArgs a, const DecodeRow* __restrict__ rows, const
   }
 }
 
-// Log-sum-exp merge of the rows split across groups.  Wave k Hkv + h owns
+// Log-sum-exp merge of the rows split across groups (and the zeroing of
+// decode rows without a visible key).  Wave k Hkv + h owns
 // kv head h of the row that crosses the boundary after group k if that row
 // starts inside group k's range; its partials sit in wave k Hkv + h (slot 0
 // if the row is the group's first segment, else slot 1) and in waves
@@ -479,22 +613,41 @@ void paged_decode_kernel(DecodeArgs a, const DecodeRow* __restrict__ rows, const
 // head 4 p + l / 16 of the group (pass p) and head_dim elements 8 (l % 16) ..
 // + 7; one pass over the partials keeps a running max, sum and output, with
 // the loads of four partials in flight at a time.
-__global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a, const DecodeRow* __restrict__ rows,
-                                                         const WaveStart* __restrict__ starts) {
+__global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a, int groups, const int32_t* __restrict__ cu_q,
+                                                         const int32_t* __restrict__ cu_k) {
   const int k = blockIdx.x / a.Hkv, h = blockIdx.x - k * a.Hkv;
-  const int Kw = a.hdr->n_groups;
+  const int lane = threadIdx.x;
+  // Tiles, and the zeroing of decode rows without a visible key (row b by
+  // merge wave b % gridDim.x).
+  int T = 0;
+  for (int c0 = 0; c0 < a.B; c0 += 64) {
+    const int b = c0 + lane;
+    RowInfo ri = {false, 0, 0};
+    if (b < a.B) ri = row_info(a, cu_q, cu_k, b);
+    T += wave_sum_i(row_tiles(ri));
+    uint64_t z = __ballot(ri.dec && ri.K <= 0 && b % (int)gridDim.x == (int)blockIdx.x);
+    while (z) {
+      const int li = __builtin_ctzll(z);
+      z &= z - 1;
+      const int q0 = __builtin_amdgcn_readlane(ri.q0, li);
+      for (int i = lane; i < a.Hq * (kHeadDim / 8); i += 64) {
+        const int hq = i / (kHeadDim / 8), d = 8 * (i % (kHeadDim / 8));
+        *reinterpret_cast<u32x4*>(a.out + (int64_t)q0 * a.out_ts + (int64_t)hq * a.out_hs + d) = u32x4{0, 0, 0, 0};
+      }
+    }
+  }
+  const int Kw = T > 0 ? min(groups, max(1, T / kDecodeMinUnits)) : 0;
   if (k + 1 >= Kw) return;
-  const int T = a.hdr->n_units;
-  const WaveStart st = starts[k + 1];
-  if (st.t == 0) return;  // the boundary falls between rows
-  const DecodeRow r = rows[st.row];
-  const int first = r.prefix;  // the row's first tile
+  Chunk ch;
+  Cursor r;
+  int first;  // the first tile of the row at the boundary after group k
+  locate_tile(a, cu_q, cu_k, (int)((int64_t)(k + 1) * T / Kw), ch, r, first);
+  if (r.t == 0) return;  // the boundary falls between rows
   const int sk = (int)((int64_t)k * T / Kw);
   if (first < sk) return;  // started in an earlier group, which merges it
   const int last = first + r.n - 1;
   const int k_last = (int)(((int64_t)(last + 1) * Kw - 1) / T);
   const int slot_k = first != sk ? 1 : 0;
-  const int lane = threadIdx.x;
   const int j = lane & 15;
   for (int c0 = 0; c0 < a.g; c0 += 4) {
     const int c = c0 + (lane >> 4);
@@ -541,37 +694,41 @@ int64_t decode_workspace_bytes(int max_waves, int group) {
   return (int64_t)max_waves * 2 * group * (kHeadDim + 2) * (int64_t)sizeof(float);
 }
 
-int launch_decode(const AttnParams& P, const Plan& plan, int waves, void* partials, hipStream_t stream) {
+int launch_decode(const AttnParams& P, int max_waves, int waves, void* partials, hipStream_t stream) {
   DecodeArgs a;
   a.q = (const uint16_t*)P.q; a.q_ts = P.q_ts; a.q_hs = P.q_hs;
   a.kc = P.kc; a.vc = P.vc; a.ks = P.ks; a.vs = P.vs;
   a.bt_stride = (int)P.bt_stride; a.NB = (int)P.NB;
   a.Hq = P.Hq; a.Hkv = P.Hkv; a.g = P.Hq / P.Hkv; a.bs = P.bs;
   a.scale_log2 = P.softmax_scale * 1.4426950408889634f;
+  a.cu_q = P.cu_q; a.cu_k = P.cu_k; a.B = P.B; a.T = P.T;
   a.out = (uint16_t*)P.out; a.out_ts = P.out_ts; a.out_hs = P.out_hs;
-  a.hdr = plan.hdr;
   a.ws_o = (float*)partials;
-  a.ws_ml = a.ws_o + (int64_t)plan.max_waves * 2 * a.g * kHeadDim;
+  a.ws_ml = a.ws_o + (int64_t)max_waves * 2 * a.g * kHeadDim;
   if (waves <= 0) return NVS_OK;
   dim3 grid(waves), block(64);
   switch (P.cache_dtype) {
     case NVS_DTYPE_BF16:
-      hipLaunchKernelGGL(paged_decode_kernel<NVS_DTYPE_BF16>, grid, block, 0, stream, a, plan.rows, plan.starts, P.bt);
+      hipLaunchKernelGGL(paged_decode_kernel<NVS_DTYPE_BF16>, grid, block, 0, stream, a, P.bt, P.cu_q, P.cu_k);
       break;
     case NVS_DTYPE_INT8:
-      hipLaunchKernelGGL(paged_decode_kernel<NVS_DTYPE_INT8>, grid, block, 0, stream, a, plan.rows, plan.starts, P.bt);
+      hipLaunchKernelGGL(paged_decode_kernel<NVS_DTYPE_INT8>, grid, block, 0, stream, a, P.bt, P.cu_q, P.cu_k);
       break;
     case NVS_DTYPE_FP8_E4M3:
-      hipLaunchKernelGGL(paged_decode_kernel<NVS_DTYPE_FP8_E4M3>, grid, block, 0, stream, a, plan.rows, plan.starts,
-                         P.bt);
+      hipLaunchKernelGGL(paged_decode_kernel<NVS_DTYPE_FP8_E4M3>, grid, block, 0, stream, a, P.bt, P.cu_q,
+                         P.cu_k);
       break;
     default:
       set_error("paged_attention: decode does not serve cache dtype %d", P.cache_dtype);
       return NVS_ERR_UNSUPPORTED;
   }
   int rc = check_launch("paged_decode");
-  if (rc != NVS_OK || waves <= P.Hkv) return rc;
-  hipLaunchKernelGGL(decode_merge_kernel, dim3(waves - P.Hkv), dim3(64), 0, stream, a, plan.rows, plan.starts);
+  if (rc != NVS_OK) return rc;
+  // The merge also zeroes decode rows without a visible key, so it runs even
+  // when a single group cannot leave split rows.
+  const int groups = waves / P.Hkv;
+  hipLaunchKernelGGL(decode_merge_kernel, dim3(std::max(groups - 1, 1) * P.Hkv), dim3(64), 0, stream, a, groups,
+                     P.cu_q, P.cu_k);
   return check_launch("decode_merge");
 }
 

@@ -1,5 +1,5 @@
-// Planning kernel: compact decode / prefill work lists from cu_seqlens, on
-// the device and without a host round trip.
+// Planning kernel: the prefill work list from cu_seqlens, on the device and
+// without a host round trip.
 #include "nvs_common.h"
 #include "attention_common.h"
 
@@ -11,10 +11,6 @@ struct PlanArgs {
   int B;
   int64_t T;
   int paged;
-  int Hq, Hkv;
-  int waves;  // decode waves launched (<= plan.max_waves)
-  uint16_t* out;  // rows without a visible key are zeroed here
-  int64_t out_ts, out_hs;
   Plan plan;
 };
 
@@ -65,95 +61,23 @@ constexpr int kPlanFastLevels = 512;  // prefill tiles per row the one-pass orde
 
 __global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanArgs a) {
   __shared__ int scan_lds[kPlanWaves];
-  __shared__ int row_incl[kPlanThreads];  // inclusive unit prefix of the chunk's decode rows
-  __shared__ int row_idx[kPlanThreads];   // decode row index of the chunk's rows
-  __shared__ int row_n[kPlanThreads];     // tiles of the chunk's decode rows
   __shared__ int lev_cnt[kPlanFastLevels * kPlanWaves];
   __shared__ int lev_off[kPlanFastLevels];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const Plan& pl = a.plan;
   if (tid < 8) pl.hdr->prefill_next[tid] = 0;
 
-  // ---- decode rows, 1024 rows at a time: compact index and unit prefix by
-  // two block scans.  A decode row without a visible key gets no units and no
-  // entry; its output is zeroed here.
-  int nrows = 0, units = 0, deepest = 0, np0 = 0;
-  for (int b0 = 0; b0 < a.B; b0 += kPlanThreads) {
-    bool dec;
-    int np, q0, kl, tot_r, tot_u;
-    row_work(a, b0 + tid, dec, np, q0, kl);
-    if (b0 == 0) np0 = np;
-    deepest = max(deepest, np);
-    const int n = dec && kl > 0 ? (kl + kDecodeTile - 1) / kDecodeTile : 0;
-    const int u = n;
-    const int ir = block_scan_1024(n > 0 ? 1 : 0, scan_lds, tot_r);
-    const int iu = block_scan_1024(u, scan_lds, tot_u);
-    if (n > 0) {
-      DecodeRow r;
-      r.b = b0 + tid;
-      r.q0 = q0;
-      r.K = kl;
-      r.n = n;
-      r.prefix = units + iu - u;
-      r.pad[0] = r.pad[1] = r.pad[2] = 0;
-      pl.rows[nrows + ir - 1] = r;
-    } else if (dec) {
-      for (int i = 0; i < a.Hq * (kHeadDim / 2); ++i) {
-        const int hq = i / (kHeadDim / 2), d = 2 * (i % (kHeadDim / 2));
-        *reinterpret_cast<uint32_t*>(a.out + (int64_t)q0 * a.out_ts + (int64_t)hq * a.out_hs + d) = 0u;
-      }
-    }
-    nrows += tot_r;
-    units += tot_u;
-  }
-  // Wave groups: Kw groups of Hkv waves (one per kv head), at most the
-  // launched waves and at least kDecodeMinUnits tiles per group.
-  const int ngroups = units > 0 ? (int)min((int64_t)(a.waves / a.Hkv), max((int64_t)1, (int64_t)units / kDecodeMinUnits)) : 0;
-  if (tid == 0) {
-    pl.hdr->n_rows = nrows;
-    pl.hdr->n_units = units;
-    pl.hdr->n_groups = ngroups;
-  }
-
-  // ---- group starts: group k begins at tile s_k = floor(k T / Kw), inside
-  // the first row whose inclusive tile prefix exceeds s_k.
-  if (ngroups > 0) {
-    int rbase = 0, ubase = 0;
-    for (int b0 = 0; b0 < a.B; b0 += kPlanThreads) {
-      bool dec;
-      int np, q0, kl, tot_r, tot_u;
-      row_work(a, b0 + tid, dec, np, q0, kl);
-      const int n = dec && kl > 0 ? (kl + kDecodeTile - 1) / kDecodeTile : 0;
-      const int u = n;
-      const int ir = block_scan_1024(n > 0 ? 1 : 0, scan_lds, tot_r);
-      const int iu = block_scan_1024(u, scan_lds, tot_u);
-      row_incl[tid] = ubase + iu;
-      row_idx[tid] = rbase + ir - 1;
-      row_n[tid] = n;
-      __syncthreads();
-      for (int k = tid; k < ngroups; k += kPlanThreads) {
-        const int sw = (int)((int64_t)k * units / ngroups);
-        if (sw < ubase || sw >= ubase + tot_u) continue;
-        int lo = 0, hi = kPlanThreads - 1;  // first r with row_incl[r] > sw
-        while (lo < hi) {
-          const int mid = (lo + hi) >> 1;
-          if (row_incl[mid] > sw) hi = mid; else lo = mid + 1;
-        }
-        WaveStart st;
-        st.row = row_idx[lo];
-        st.t = sw - (row_incl[lo] - row_n[lo]);
-        st.pad[0] = st.pad[1] = 0;
-        pl.starts[k] = st;
-      }
-      rbase += tot_r;
-      ubase += tot_u;
-      __syncthreads();
-    }
-  }
-
   // ---- prefill tiles level by level from the deepest query tile down, so
   // the heaviest tiles (most keys under the causal mask) of every row come
   // first; rows in order within a level.
+  int deepest = 0, np0 = 0;
+  for (int b0 = 0; b0 < a.B; b0 += kPlanThreads) {
+    bool dec;
+    int np, q0, kl;
+    row_work(a, b0 + tid, dec, np, q0, kl);
+    if (b0 == 0) np0 = np;
+    deepest = max(deepest, np);
+  }
   int nlev;
   {
     int v = deepest;
@@ -231,19 +155,13 @@ int device_slots(int per_cu) {
   return g_cus[dev] * per_cu;
 }
 
-int launch_plan(const AttnParams& P, const Plan& plan, bool paged, int decode_waves, hipStream_t stream) {
+int launch_plan(const AttnParams& P, const Plan& plan, bool paged, hipStream_t stream) {
   PlanArgs a;
   a.cu_q = P.cu_q;
   a.cu_k = P.cu_k;
   a.B = P.B;
   a.T = P.T;
   a.paged = paged ? 1 : 0;
-  a.Hq = P.Hq;
-  a.Hkv = P.Hkv;
-  a.waves = decode_waves;
-  a.out = (uint16_t*)P.out;
-  a.out_ts = P.out_ts;
-  a.out_hs = P.out_hs;
   a.plan = plan;
   hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(1024), 0, stream, a);
   return check_launch("plan");
