@@ -21,7 +21,6 @@ from __future__ import annotations
 import argparse
 import json
 import os
-import statistics
 import sys
 import time
 
@@ -37,20 +36,22 @@ def log(*a):
 
 def timed_steps(fn, steps: int, warmup: int):
     """W untimed calls, then K timed calls bracketed by synchronize; returns
-    (ms per step, per-call event ms list measured on the current stream)."""
+    (wall ms per step, ms per step from one pair of HIP events around the K
+    calls on the current stream).  One pair for the whole region keeps the
+    event packets' own cost out of the per-step figure."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
-    for a, b in ev:
-        a.record(stream)
+    e0.record(stream)
+    for _ in range(steps):
         fn()
-        b.record(stream)
+    e1.record(stream)
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) * 1e3 / steps
-    return wall, [a.elapsed_time(b) for a, b in ev]
+    return wall, e0.elapsed_time(e1) / steps
 
 
 def attention_only(wl):
@@ -70,8 +71,7 @@ def bench_decode(steps, warmup):
     wl = W.decode_8b("cuda")
     nbytes = wl.decode_bytes()
     ms_step, _ = timed_steps(step(wl), steps, warmup)
-    _, ev = timed_steps(attention_only(wl), steps, warmup)
-    ms_attn = statistics.median(ev)
+    _, ms_attn = timed_steps(attention_only(wl), steps, warmup)
     res = {
         "bytes": nbytes,
         "ms_per_step": ms_step,
@@ -91,8 +91,7 @@ def bench_prefill(steps, warmup):
     wl = W.prefill_8b("cuda")
     flops = wl.prefill_flops()
     ms_step, _ = timed_steps(step(wl), steps, warmup)
-    _, ev = timed_steps(attention_only(wl), steps, warmup)
-    ms_attn = statistics.median(ev)
+    _, ms_attn = timed_steps(attention_only(wl), steps, warmup)
     res = {
         "workload": "prefill_8b: 32q/8kv heads, D128, bs256, 16 seqs, new U[512,4096] over 0-8 cached blocks, seed 2",
         "flops": flops,
@@ -116,8 +115,7 @@ def bench_quant(steps, warmup):
         wl = W.decode_quant("cuda", kv=kv)
         nbytes = wl.decode_bytes()
         ms_step, _ = timed_steps(step(wl), steps, warmup)
-        _, ev = timed_steps(attention_only(wl), steps, warmup)
-        ms_attn = statistics.median(ev)
+        _, ms_attn = timed_steps(attention_only(wl), steps, warmup)
         out[kv] = {
             "bytes": nbytes,
             "ms_per_step": ms_step,

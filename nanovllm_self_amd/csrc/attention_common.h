@@ -78,8 +78,8 @@ __device__ __forceinline__ bf16x8 codes8_to_bf16x8(uint32_t lo, uint32_t hi) {
 // (each costs the dispatcher several nanoseconds; an upper-bound grid is
 // mostly empty on ragged batches).
 //   prefill list: b * ntq + qt, one entry per (q_len > 1 row, tile of
-//                 prefill_positions(g) query positions), every row's tiles in
-//                 descending qt (heaviest first).
+//                 prefill_positions(g) query positions), row by row, each
+//                 row's tiles in descending qt (heaviest first).
 // ---------------------------------------------------------------------------
 
 // Prefill work item: one 8-wave work-group serves up to 8 query heads of one

@@ -57,86 +57,25 @@ __device__ __forceinline__ void row_work(const PlanArgs& a, int b, bool& dec, in
 
 constexpr int kPlanThreads = 1024;
 constexpr int kPlanWaves = kPlanThreads / 64;
-constexpr int kPlanFastLevels = 512;  // prefill tiles per row the one-pass ordering serves
 
 __global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanArgs a) {
   __shared__ int scan_lds[kPlanWaves];
-  __shared__ int lev_cnt[kPlanFastLevels * kPlanWaves];
-  __shared__ int lev_off[kPlanFastLevels];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x;
   const Plan& pl = a.plan;
   if (tid < 8) pl.hdr->prefill_next[tid] = 0;
-
-  // ---- prefill tiles level by level from the deepest query tile down, so
-  // the heaviest tiles (most keys under the causal mask) of every row come
-  // first; rows in order within a level.
-  int deepest = 0, np0 = 0;
+  // ---- prefill tiles row by row (1024 rows per step: an exclusive scan of
+  // the rows' tile counts), each row's tiles deepest first (most keys under
+  // the causal mask).  Row-major order keeps the work-groups of an XCD on the
+  // same sequence at the same time, so the K/V tiles they all read come
+  // from HBM once and from L2 after that.
+  int base = 0;
   for (int b0 = 0; b0 < a.B; b0 += kPlanThreads) {
     bool dec;
-    int np, q0, kl;
+    int np, q0, kl, tot;
     row_work(a, b0 + tid, dec, np, q0, kl);
-    if (b0 == 0) np0 = np;
-    deepest = max(deepest, np);
-  }
-  int nlev;
-  {
-    int v = deepest;
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = max(v, __shfl_xor(v, off, 64));
-    if (lane == 0) scan_lds[w] = v;
-    __syncthreads();
-    nlev = 0;
-#pragma unroll
-    for (int i = 0; i < kPlanWaves; ++i) nlev = max(nlev, scan_lds[i]);
-    __syncthreads();
-  }
-  if (a.B <= kPlanThreads && nlev <= kPlanFastLevels) {
-    // One pass: per (level, wave) counts by ballot, their prefixes over waves
-    // and over deeper levels, then each row writes its tiles directly.
-    for (int lev = 0; lev < nlev; ++lev) {
-      const int c = __popcll(__ballot(np0 > lev));
-      if (lane == 0) lev_cnt[lev * kPlanWaves + w] = c;
-    }
-    __syncthreads();
-    for (int lev = tid; lev < nlev; lev += kPlanThreads) {
-      int run = 0;
-#pragma unroll
-      for (int x = 0; x < kPlanWaves; ++x) {
-        const int c = lev_cnt[lev * kPlanWaves + x];
-        lev_cnt[lev * kPlanWaves + x] = run;
-        run += c;
-      }
-      lev_off[lev] = run;  // level total, turned into its offset below
-    }
-    __syncthreads();
-    const int lev = nlev - 1 - tid;  // deepest level first
-    const int v = lev >= 0 ? lev_off[lev] : 0;
-    int total;
-    const int incl = block_scan_1024(v, scan_lds, total);
-    if (lev >= 0) lev_off[lev] = incl - v;
-    __syncthreads();
-    const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    for (int l = 0; l < nlev; ++l) {
-      const uint64_t m = __ballot(np0 > l);
-      if (np0 > l)
-        pl.plist[lev_off[l] + lev_cnt[l * kPlanWaves + w] + __popcll(m & below)] = tid * pl.ntq + l;
-    }
-    if (tid == 0) pl.hdr->n_prefill = total;
-    return;
-  }
-  // General case: one block scan per (level, chunk of rows).
-  int base = 0;
-  for (int lev = nlev - 1; lev >= 0; --lev) {
-    for (int b0 = 0; b0 < a.B; b0 += kPlanThreads) {
-      const int b = b0 + tid;
-      bool dec;
-      int np, q0, kl, tot;
-      row_work(a, b, dec, np, q0, kl);
-      const int f = np > lev ? 1 : 0;
-      const int incl = block_scan_1024(f, scan_lds, tot);
-      if (f) pl.plist[base + incl - 1] = b * pl.ntq + lev;
-      base += tot;
-    }
+    const int incl = block_scan_1024(np, scan_lds, tot);
+    for (int i = 0; i < np; ++i) pl.plist[base + incl - np + i] = (b0 + tid) * pl.ntq + (np - 1 - i);
+    base += tot;
   }
   if (tid == 0) pl.hdr->n_prefill = base;
 }
