@@ -72,8 +72,7 @@ template <int KV>
 struct DecodeTile {
   u32x4 k[2][2];  // [t][half]: 32 codes, d = 32 grp + 16 half .. +15
   u32x2 v[8];     // [e]: 8 codes, d = 8 col .. +7
-  float ksc[8];   // scales of the 8 keys the lane owns (slot order)
-  float vsc[8];
+  float sc;       // lanes 0-31: k scale of key l; lanes 32-63: v scale of key l - 32
   bool has;
 };
 
@@ -95,7 +94,6 @@ constexpr int kKGroupStride = (KV == NVS_DTYPE_BF16) ? 8 : 32;
 struct LaneOffsets {
   uint32_t k;   // key col, d = 8 grp (bf16) / 32 grp (codes)
   uint32_t v;   // key 4 grp, d = 8 col
-  uint32_t sc;  // scale of key 4 grp
 };
 
 template <int KV>
@@ -105,7 +103,6 @@ __device__ __forceinline__ LaneOffsets lane_offsets(int Hkv, int col, int grp) {
   LaneOffsets o;
   o.k = (uint32_t)col * row + kKGroupStride<KV> * grp * ESZ;
   o.v = (uint32_t)(4 * grp) * row + 8 * col * ESZ;
-  o.sc = (uint32_t)(4 * grp) * Hkv * 4;
   return o;
 }
 
@@ -135,15 +132,12 @@ __device__ __forceinline__ void decode_load(DecodeTile<KV>& T, const DecodeArgs&
       T.k[t][0] = *reinterpret_cast<const u32x4*>(kb + 16 * t * rowb + lo.k);
       T.k[t][1] = *reinterpret_cast<const u32x4*>(kb + 16 * t * rowb + 16 + lo.k);
     }
-    const char* ksb = (const char*)(a.ks + row0);
-    const char* vsb = (const char*)(a.vs + row0);
-    const int64_t srow = (int64_t)a.Hkv * 4;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      T.v[e] = *reinterpret_cast<const u32x2*>(vb + slot_key(e, 0) * rowb + lo.v);
-      T.ksc[e] = *reinterpret_cast<const float*>(ksb + slot_key(e, 0) * srow + lo.sc);
-      T.vsc[e] = *reinterpret_cast<const float*>(vsb + slot_key(e, 0) * srow + lo.sc);
-    }
+    for (int e = 0; e < 8; ++e) T.v[e] = *reinterpret_cast<const u32x2*>(vb + slot_key(e, 0) * rowb + lo.v);
+    // One scale per lane; the compute hands each lane its keys' scales with
+    // cross-lane reads.
+    const int lane = threadIdx.x;
+    T.sc = ((lane < 32) ? a.ks : a.vs)[row0 + (int64_t)(lane & 31) * a.Hkv];
   }
 }
 
@@ -162,11 +156,8 @@ __device__ __forceinline__ void zero_tile(DecodeTile<KV>& T) {
 #pragma unroll
     for (int t = 0; t < 2; ++t) T.k[t][0] = T.k[t][1] = u32x4{0, 0, 0, 0};
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      T.v[e] = u32x2{0, 0};
-      T.ksc[e] = 0.0f;
-      T.vsc[e] = 0.0f;
-    }
+    for (int e = 0; e < 8; ++e) T.v[e] = u32x2{0, 0};
+    T.sc = 0.0f;
   }
 }
 
@@ -205,6 +196,17 @@ __device__ __forceinline__ void decode_tile_compute(const DecodeTile<KV>& T, con
       s[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qop[st], s[t], 0, 0, 0);
     }
   }
+  // ---- per-key scales of quantised caches: slot e of this lane is key
+  // slot_key(e, grp), whose k scale lane slot_key(e, grp) holds and whose v
+  // scale lane 32 + slot_key(e, grp) holds.
+  float ksc[8], vsc[8];
+  if constexpr (KV != NVS_DTYPE_BF16) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      ksc[e] = __shfl(T.sc, slot_key(e, grp), 64);
+      vsc[e] = __shfl(T.sc, 32 + slot_key(e, grp), 64);
+    }
+  }
   // ---- online softmax (log2 domain) -----------------------------------------
   bool valid[8];
 #pragma unroll
@@ -213,7 +215,7 @@ __device__ __forceinline__ void decode_tile_compute(const DecodeTile<KV>& T, con
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     float f = scale_log2;
-    if constexpr (KV != NVS_DTYPE_BF16) f *= T.ksc[e];
+    if constexpr (KV != NVS_DTYPE_BF16) f *= ksc[e];
     float x = s[e >> 2][e & 3] * f;
     if constexpr (MASKED) x = valid[e] ? x : -INFINITY;  // outside the partition
     sv[e] = x;
@@ -237,7 +239,7 @@ __device__ __forceinline__ void decode_tile_compute(const DecodeTile<KV>& T, con
     const float p = fast_exp2(sv[e] - m_run);
     l_run += p;
     float pw = p;
-    if constexpr (KV != NVS_DTYPE_BF16) pw = p * T.vsc[e];
+    if constexpr (KV != NVS_DTYPE_BF16) pw = p * vsc[e];
     if constexpr (MASKED) pw = valid[e] ? pw : 0.0f;
     pv[e] = pw;
   }
