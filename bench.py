@@ -282,7 +282,7 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "paged_attention decode call (split-K decode + partition merge)",
+            "kernel": "paged_attention decode call (stream-K decode kernel + merge of split rows)",
             "achieved": round(dec["gbs_attention"], 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
