@@ -136,11 +136,14 @@ int nvs_gather_kvcache(const void* k_cache, const void* v_cache,
 
 /*
  * Workspace (bytes) that nvs_paged_attention / nvs_varlen_attention need for
- * a batch with these bounds: the work plan the device builds from
- * cu_seqlens (compact lists of decode partitions and prefill query tiles)
- * followed by the split-K decode partials.  The workspace must be 256-byte
- * aligned; it needs no initialisation and is scratch between calls; calls
- * that share one workspace must be ordered on one stream.
+ * a batch with these bounds: the prefill work plan the device builds from
+ * cu_seqlens (a 256-byte header and the list of prefill query tiles)
+ * followed by the decode partials (two slots of (num_heads / num_kv_heads) x
+ * (head_dim + 2) floats per decode wave, for rows whose keys are split
+ * across wave groups).  num_kv_heads <= 0 asks for an upper bound over every
+ * kv-head count.  The workspace must be 256-byte aligned; it needs no
+ * initialisation and is scratch between calls; calls that share one
+ * workspace must be ordered on one stream.
  */
 int64_t nvs_attention_workspace_bytes(int num_seqs, int max_seqlen_q,
                                       int max_seqlen_k, int num_heads,

@@ -43,18 +43,20 @@ static int prefill_tiles(int max_seqlen_q, int pbm) {
   return t < 1 ? 1 : t;
 }
 
-// Query heads per kv head (1 when the pair is invalid: sizing only).
-static int group_of(int num_heads, int num_kv_heads) {
-  return (num_kv_heads > 0 && num_heads % num_kv_heads == 0) ? num_heads / num_kv_heads : 1;
-}
-
 // Workspace: the prefill plan, then the decode partials (256-byte aligned).
+// With an unknown kv-head count (num_kv_heads <= 0, or not dividing
+// num_heads) both parts are sized for their worst case: the smallest prefill
+// tile, and one kv head whose group is every query head (waves x group is
+// largest there).
 int64_t attention_workspace_bytes(int num_seqs, int max_seqlen_q, int max_seqlen_k, int num_heads,
                                   int num_kv_heads) {
   if (num_seqs <= 0 || num_heads <= 0) return 0;
-  const int waves = decode_wave_cap(num_seqs, max_seqlen_k, num_kv_heads);
+  const bool known = num_kv_heads > 0 && num_heads % num_kv_heads == 0;
+  const int hk = known ? num_kv_heads : 1;
+  const int group = known ? num_heads / num_kv_heads : num_heads;
+  const int waves = decode_wave_cap(num_seqs, max_seqlen_k, hk);
   const int ntq = prefill_tiles(max_seqlen_q, prefill_pbm(num_heads, num_kv_heads));
-  return align256(plan_bytes(num_seqs, ntq)) + decode_workspace_bytes(waves, group_of(num_heads, num_kv_heads));
+  return align256(plan_bytes(num_seqs, ntq)) + decode_workspace_bytes(waves, group);
 }
 
 static Plan make_plan(void* ws, const AttnParams& P) {

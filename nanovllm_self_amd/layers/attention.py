@@ -56,10 +56,13 @@ def attention_workspace(device: torch.device, nbytes: int) -> torch.Tensor | Non
 
 
 def reserve_attention_workspace(num_seqs: int, max_seqlen_q: int, max_seqlen_k: int, num_heads: int,
-                                device) -> None:
+                                device, num_kv_heads: int = 0) -> None:
     """Pre-size the workspace for batches up to these bounds (for example
-    before capturing a graph, where it cannot grow)."""
-    n = _lib.load().nvs_attention_workspace_bytes(num_seqs, max_seqlen_q, max_seqlen_k, num_heads, 0, 128, 0)
+    before capturing a graph, where it cannot grow).  num_kv_heads = 0 sizes
+    for every kv-head count (an upper bound); passing the layer's count
+    reserves exactly what its calls need."""
+    n = _lib.load().nvs_attention_workspace_bytes(num_seqs, max_seqlen_q, max_seqlen_k, num_heads, num_kv_heads,
+                                                  128, 0)
     attention_workspace(torch.device(device), int(n))
 
 

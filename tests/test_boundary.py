@@ -180,13 +180,14 @@ def test_workspace_bytes():
     by the decode partials: two slots of g x (128 + 2) floats per decode
     wave.  Decode waves come in groups of Hkv: at most 2048 waves, and at
     most one group per 4 32-key tiles the batch can hold, rounded up to a
-    multiple of 8 groups."""
+    multiple of 8 groups.  An unknown kv-head count (0) gets an upper bound."""
     lib = _lib.load()
     a256 = lambda x: (x + 255) // 256 * 256
 
     def expect(B, max_q, max_k, Hq, Hkv):
-        g = Hq // Hkv if Hkv > 0 and Hq % Hkv == 0 else 1
-        hk = max(Hkv, 1)
+        known = Hkv > 0 and Hq % Hkv == 0
+        g = Hq // Hkv if known else Hq  # unknown: one kv head, every query head in its group
+        hk = Hkv if known else 1
         tiles = B * ((max_k + 31) // 32)
         groups = ((tiles + 3) // 4 + 7) // 8 * 8
         waves = hk * min(2048 // hk, max(1, groups))
@@ -206,3 +207,15 @@ def test_workspace_bytes():
     for Hq, Hkv in ((32, 8), (64, 4), (8, 8), (32, 0)):
         assert lib.nvs_attention_workspace_bytes(16, 4096, 256, Hq, Hkv, 128, 256) == expect(16, 4096, 256, Hq, Hkv)
     assert expect(16, 4096, 256, 32, 8) == a256(256 + a256(16 * 64 * 4)) + 256 * 2 * 4 * 520
+
+
+def test_workspace_unknown_kv_heads_is_upper_bound():
+    """num_kv_heads = 0 (what a caller reserving ahead of time may pass) must
+    size the workspace for every kv-head count the call could have."""
+    lib = _lib.load()
+    for B, max_q, max_k in ((1, 1, 32), (8, 1, 1000), (64, 1, 8192), (300, 1, 4096), (16, 4096, 20000), (4, 2048, 32768)):
+        for Hq in (8, 16, 32, 64):
+            bound = lib.nvs_attention_workspace_bytes(B, max_q, max_k, Hq, 0, 128, 256)
+            for Hkv in (h for h in (1, 2, 4, 8, 16, 32, 64) if Hq % h == 0 and Hq // h <= 16):
+                need = lib.nvs_attention_workspace_bytes(B, max_q, max_k, Hq, Hkv, 128, 256)
+                assert bound >= need, (B, max_q, max_k, Hq, Hkv, bound, need)
