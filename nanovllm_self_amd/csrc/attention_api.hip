@@ -27,6 +27,9 @@ static int validate_common(const AttnParams& P, const char* who) {
               "%s: q rows must be 16-byte aligned", who);
   NVS_REQUIRE(P.out_ts % 8 == 0 && P.out_hs % 8 == 0 && ((uintptr_t)P.out % 16) == 0,
               NVS_ERR_INVALID, "%s: out rows must be 16-byte aligned", who);
+  // The decode kernel addresses a group's heads with 32-bit lane offsets.
+  NVS_REQUIRE(P.q_hs >= 0 && P.q_hs < (1ll << 26) && P.out_hs >= 0 && P.out_hs < (1ll << 26),
+              NVS_ERR_UNSUPPORTED, "%s: head strides must lie in [0, 2^26) elements", who);
   return NVS_OK;
 }
 

@@ -12,7 +12,7 @@ constexpr int kHeadDim = 128;    // head_dim served by the attention kernels
 constexpr int kDecodeWavesPerEU = NVS_DECODE_WAVES_PER_EU;  // decode waves per SIMD
 constexpr int kDecodeTile = 32;         // keys per decode tile (one unit of decode work)
 constexpr int kDecodeMaxWaves = 2048;   // decode waves per call at most (256 CUs x 8)
-constexpr int kDecodeMinUnits = 4;      // fewest units a decode wave is given
+constexpr int kDecodeMinUnits = 4;      // fewest tiles a decode group is given
 
 // 2^x on the hardware transcendental unit (v_exp_f32); 2^-inf = 0.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }

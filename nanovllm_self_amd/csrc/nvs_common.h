@@ -34,6 +34,19 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // ---------------------------------------------------------------------------
+// Per-lane address offsets.  global_load/store take a 64-bit wave-uniform base
+// in scalar registers plus a 32-bit lane offset when the address is built as
+// base + zext(offset) in the same block.  A loop-invariant offset would be
+// zero-extended once before the loop and kept as a 64-bit lane address in two
+// registers; passing it through an empty asm at the use keeps the extension
+// in the block, so the offset stays one 32-bit register.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t lane_off(uint32_t x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
+// ---------------------------------------------------------------------------
 // Scalar conversions.  Widening bf16/fp16 -> fp32 is exact; narrowing uses
 // round-to-nearest-even, the rounding torch's .to(dtype) applies.
 // ---------------------------------------------------------------------------

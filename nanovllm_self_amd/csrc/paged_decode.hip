@@ -108,6 +108,7 @@ __device__ __forceinline__ LaneOffsets lane_offsets(int Hkv, int col, int grp) {
 
 // Loads of one 32-key tile of kv head h whose first key sits at offset koff
 // of pool block blk (-1: missing; the loads then read block 0, in bounds).
+// Every address is a wave-uniform row base plus a 32-bit lane offset.
 template <int KV>
 __device__ __forceinline__ void decode_load(DecodeTile<KV>& T, const DecodeArgs& a, const LaneOffsets& lo,
                                             int blk, int koff, int h) {
@@ -117,27 +118,28 @@ __device__ __forceinline__ void decode_load(DecodeTile<KV>& T, const DecodeArgs&
   const int64_t rowb = (int64_t)a.Hkv * kHeadDim * ESZ;  // bytes per token row
   const char* kb = (const char*)a.kc + row0 * kHeadDim * ESZ;
   const char* vb = (const char*)a.vc + row0 * kHeadDim * ESZ;
+  const uint32_t ok = lane_off(lo.k), ov = lane_off(lo.v);
   if constexpr (KV == NVS_DTYPE_BF16) {
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int s = 0; s < 4; ++s)
-        T.k[t][s] = *reinterpret_cast<const u32x4*>(kb + 16 * t * rowb + 64 * s + lo.k);
+      for (int s = 0; s < 4; ++s) T.k[t][s] = *reinterpret_cast<const u32x4*>(kb + 16 * t * rowb + 64 * s + ok);
 #pragma unroll
-    for (int e = 0; e < 8; ++e)
-      T.v[e] = *reinterpret_cast<const u32x4*>(vb + slot_key(e, 0) * rowb + lo.v);
+    for (int e = 0; e < 8; ++e) T.v[e] = *reinterpret_cast<const u32x4*>(vb + slot_key(e, 0) * rowb + ov);
   } else {
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      T.k[t][0] = *reinterpret_cast<const u32x4*>(kb + 16 * t * rowb + lo.k);
-      T.k[t][1] = *reinterpret_cast<const u32x4*>(kb + 16 * t * rowb + 16 + lo.k);
+      T.k[t][0] = *reinterpret_cast<const u32x4*>(kb + 16 * t * rowb + ok);
+      T.k[t][1] = *reinterpret_cast<const u32x4*>(kb + 16 * t * rowb + 16 + ok);
     }
 #pragma unroll
-    for (int e = 0; e < 8; ++e) T.v[e] = *reinterpret_cast<const u32x2*>(vb + slot_key(e, 0) * rowb + lo.v);
-    // One scale per lane; the compute hands each lane its keys' scales with
+    for (int e = 0; e < 8; ++e) T.v[e] = *reinterpret_cast<const u32x2*>(vb + slot_key(e, 0) * rowb + ov);
+    // One scale per lane (lanes 0-31 the k scales of the tile's keys, 32-63
+    // the v scales); the compute hands each lane its keys' scales with
     // cross-lane reads.
-    const int lane = threadIdx.x;
-    T.sc = ((lane < 32) ? a.ks : a.vs)[row0 + (int64_t)(lane & 31) * a.Hkv];
+    const uint32_t so = lane_off((uint32_t)(threadIdx.x & 31) * (uint32_t)a.Hkv * 4u);
+    const char* sb = (const char*)(((threadIdx.x < 32) ? a.ks : a.vs) + row0);
+    T.sc = *reinterpret_cast<const float*>(sb + so);
   }
 }
 
@@ -160,6 +162,37 @@ __device__ __forceinline__ void zero_tile(DecodeTile<KV>& T) {
     T.sc = 0.0f;
   }
 }
+
+// Scales of a lane's 8 key slots from the tile's one-scale-per-lane register
+// (lanes 0-31: k scale of key l, lanes 32-63: v scale of key l - 32).  Slot e
+// is key slot_key(e, grp).  ds_bpermute_b32 reads lane (address + offset) / 4,
+// so all 16 reads share one address register (16 grp bytes) and carry the
+// slot's key as the instruction's offset; one wait ends the block.
+__device__ __forceinline__ void tile_scales(float sc, int grp, float (&ksc)[8], float (&vsc)[8]) {
+  const int base = 16 * grp;
+  asm("ds_bpermute_b32 %0, %16, %17 offset:0\n\t"
+      "ds_bpermute_b32 %1, %16, %17 offset:4\n\t"
+      "ds_bpermute_b32 %2, %16, %17 offset:8\n\t"
+      "ds_bpermute_b32 %3, %16, %17 offset:12\n\t"
+      "ds_bpermute_b32 %4, %16, %17 offset:64\n\t"
+      "ds_bpermute_b32 %5, %16, %17 offset:68\n\t"
+      "ds_bpermute_b32 %6, %16, %17 offset:72\n\t"
+      "ds_bpermute_b32 %7, %16, %17 offset:76\n\t"
+      "ds_bpermute_b32 %8, %16, %17 offset:128\n\t"
+      "ds_bpermute_b32 %9, %16, %17 offset:132\n\t"
+      "ds_bpermute_b32 %10, %16, %17 offset:136\n\t"
+      "ds_bpermute_b32 %11, %16, %17 offset:140\n\t"
+      "ds_bpermute_b32 %12, %16, %17 offset:192\n\t"
+      "ds_bpermute_b32 %13, %16, %17 offset:196\n\t"
+      "ds_bpermute_b32 %14, %16, %17 offset:200\n\t"
+      "ds_bpermute_b32 %15, %16, %17 offset:204\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(ksc[0]), "=&v"(ksc[1]), "=&v"(ksc[2]), "=&v"(ksc[3]), "=&v"(ksc[4]), "=&v"(ksc[5]),
+        "=&v"(ksc[6]), "=&v"(ksc[7]), "=&v"(vsc[0]), "=&v"(vsc[1]), "=&v"(vsc[2]), "=&v"(vsc[3]),
+        "=&v"(vsc[4]), "=&v"(vsc[5]), "=&v"(vsc[6]), "=&v"(vsc[7])
+      : "v"(base), "v"(sc));
+}
+static_assert(4 * (16 + 3) + 4 * 32 + 16 * 3 < 256, "scale reads stay inside the wave's 64 lanes");
 
 // v_perm_b32 selector bytes >= 0x0C produce 0x00: masked slots are zeroed
 // inside the transpose instead of by copying registers.
@@ -200,13 +233,7 @@ __device__ __forceinline__ void decode_tile_compute(const DecodeTile<KV>& T, con
   // slot_key(e, grp), whose k scale lane slot_key(e, grp) holds and whose v
   // scale lane 32 + slot_key(e, grp) holds.
   float ksc[8], vsc[8];
-  if constexpr (KV != NVS_DTYPE_BF16) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      ksc[e] = __shfl(T.sc, slot_key(e, grp), 64);
-      vsc[e] = __shfl(T.sc, 32 + slot_key(e, grp), 64);
-    }
-  }
+  if constexpr (KV != NVS_DTYPE_BF16) tile_scales(T.sc, grp, ksc, vsc);
   // ---- online softmax (log2 domain) -----------------------------------------
   bool valid[8];
 #pragma unroll
@@ -335,20 +362,47 @@ __device__ __forceinline__ int row_tiles(const RowInfo& r) {
   return r.dec && r.K > 0 ? (r.K + kDecodeTile - 1) / kDecodeTile : 0;
 }
 
-// 64 rows of the batch: lane l holds row c0 + l's tile count (0 unless it is
-// a decode row with a visible key).
-struct Chunk {
+// A scan round: the 256 rows c0 .. c0 + 255 of the batch, lane l holding
+// rows c0 + 4 l .. + 3 as the cu_seqlens entries around them (q[i], k[i] =
+// cu_seqlens_q/k[c0 + 4 l + i], i = 0..4; entries past B read entry B, so
+// those rows are empty).  A lane issues its ten loads together, so a batch
+// of up to 256 rows costs one load round trip.
+constexpr int kScanRows = 4;
+constexpr int kScanSpan = 64 * kScanRows;
+
+struct ScanRound {
   int c0;
-  int n;
+  int q[kScanRows + 1];
+  int k[kScanRows + 1];
 };
 
-__device__ __forceinline__ Chunk load_chunk(const DecodeArgs& a, const int32_t* __restrict__ cu_q,
-                                            const int32_t* __restrict__ cu_k, int c0) {
-  Chunk ch;
-  ch.c0 = c0;
-  const int b = c0 + (int)threadIdx.x;
-  ch.n = b < a.B ? row_tiles(row_info(a, cu_q, cu_k, b)) : 0;
-  return ch;
+__device__ __forceinline__ ScanRound load_round(const DecodeArgs& a, const int32_t* __restrict__ cu_q,
+                                                const int32_t* __restrict__ cu_k, int c0) {
+  ScanRound r;
+  r.c0 = c0;
+  const int b0 = c0 + kScanRows * (int)threadIdx.x;
+#pragma unroll
+  for (int i = 0; i <= kScanRows; ++i) {
+    const int b = min(b0 + i, a.B);
+    r.q[i] = cu_q[b];
+    r.k[i] = cu_k[b];
+  }
+  return r;
+}
+
+// Tiles of the row with cu_seqlens entries (q0, q1) and (k0, k1); the same
+// rule as row_info / row_tiles.
+__device__ __forceinline__ int tiles_of(const DecodeArgs& a, int q0, int q1, int k0, int k1) {
+  const int K = k1 - k0;
+  const bool dec = q1 - q0 == 1 && q0 >= 0 && (int64_t)q1 <= a.T;
+  return dec && K > 0 ? (K + kDecodeTile - 1) / kDecodeTile : 0;
+}
+
+__device__ __forceinline__ int lane_tiles(const DecodeArgs& a, const ScanRound& r) {
+  int n = 0;
+#pragma unroll
+  for (int i = 0; i < kScanRows; ++i) n += tiles_of(a, r.q[i], r.q[i + 1], r.k[i], r.k[i + 1]);
+  return n;
 }
 
 // Wave sum; every lane holds it after the butterfly, and readfirstlane tells
@@ -370,11 +424,13 @@ __device__ __forceinline__ int wave_incl_scan(int v) {
   return v;
 }
 
-// Total decode tiles of the batch.
+// Total decode tiles of the batch; r0 receives the first scan round, which
+// locate_tile reuses.
 __device__ __forceinline__ int decode_tiles(const DecodeArgs& a, const int32_t* __restrict__ cu_q,
-                                            const int32_t* __restrict__ cu_k) {
-  int tot = 0;
-  for (int c0 = 0; c0 < a.B; c0 += 64) tot += wave_sum_i(load_chunk(a, cu_q, cu_k, c0).n);
+                                            const int32_t* __restrict__ cu_k, ScanRound& r0) {
+  r0 = load_round(a, cu_q, cu_k, 0);
+  int tot = wave_sum_i(lane_tiles(a, r0));
+  for (int c0 = kScanSpan; c0 < a.B; c0 += kScanSpan) tot += wave_sum_i(lane_tiles(a, load_round(a, cu_q, cu_k, c0)));
   return tot;
 }
 
@@ -387,50 +443,57 @@ struct Cursor {
                     // incrementally: a division by block_size would be VALU)
 };
 
-// Cursor c at lane li of chunk ch; the row's output row and key count are
-// scalar loads.
-__device__ __forceinline__ void set_row(const DecodeArgs& a, const int32_t* __restrict__ cu_q,
-                                        const int32_t* __restrict__ cu_k, Cursor& c, const Chunk& ch, int li) {
-  c.b = ch.c0 + li;
-  c.n = __builtin_amdgcn_readlane(ch.n, li);
-  c.q0 = cu_q[c.b];
-  c.K = cu_k[c.b + 1] - cu_k[c.b];
-}
-
-// The decode row and tile of tile index s (< T): the chunk holding the row
-// and a cursor at it.  Also returns the row's first tile index.
+// The decode row and tile of tile index s (< T), and the row's first tile
+// index.  r0 is the first scan round (rows 0 .. 255); later rounds are loaded
+// as the search reaches them.  The row is read from the found lane's
+// registers, so the cursor needs no further loads.
 __device__ __forceinline__ void locate_tile(const DecodeArgs& a, const int32_t* __restrict__ cu_q,
-                                            const int32_t* __restrict__ cu_k, int s, Chunk& ch, Cursor& c,
-                                            int& first) {
+                                            const int32_t* __restrict__ cu_k, int s, const ScanRound& r0,
+                                            Cursor& c, int& first) {
   int base = 0;
-  for (int c0 = 0; c0 < a.B; c0 += 64) {
-    ch = load_chunk(a, cu_q, cu_k, c0);
-    const int incl = base + wave_incl_scan(ch.n);
+  for (int c0 = 0; c0 < a.B; c0 += kScanSpan) {
+    const ScanRound rd = c0 == 0 ? r0 : load_round(a, cu_q, cu_k, c0);
+    const int nl = lane_tiles(a, rd);
+    const int incl = base + wave_incl_scan(nl);
     const uint64_t m = __ballot(incl > s);
     if (m) {
       const int li = __builtin_amdgcn_readfirstlane(__builtin_ctzll(m));
-      set_row(a, cu_q, cu_k, c, ch, li);
-      first = __builtin_amdgcn_readlane(incl, li) - c.n;
+      int e = __builtin_amdgcn_readlane(incl, li) - __builtin_amdgcn_readlane(nl, li);
+      int q[kScanRows + 1], k[kScanRows + 1];
+#pragma unroll
+      for (int i = 0; i <= kScanRows; ++i) {
+        q[i] = __builtin_amdgcn_readlane(rd.q[i], li);
+        k[i] = __builtin_amdgcn_readlane(rd.k[i], li);
+      }
+      // The lane's rows in order: the first whose tiles reach past s.  Its
+      // total exceeds s - e, so one of them does.
+      bool found = false;
+#pragma unroll
+      for (int i = 0; i < kScanRows; ++i) {
+        const int n = tiles_of(a, q[i], q[i + 1], k[i], k[i + 1]);
+        if (!found && e + n > s) {
+          found = true;
+          c.b = rd.c0 + kScanRows * li + i;
+          c.q0 = q[i];
+          c.K = k[i + 1] - k[i];
+          c.n = n;
+          first = e;
+        }
+        if (!found) e += n;
+      }
       c.t = s - first;
-      // The search result is wave-uniform; say so, so the cursor stays in
-      // scalar registers and its loads are scalar loads.
-      c.b = __builtin_amdgcn_readfirstlane(c.b);
-      c.q0 = __builtin_amdgcn_readfirstlane(c.q0);
-      c.K = __builtin_amdgcn_readfirstlane(c.K);
-      c.n = __builtin_amdgcn_readfirstlane(c.n);
-      c.t = __builtin_amdgcn_readfirstlane(c.t);
-      first = __builtin_amdgcn_readfirstlane(first);
-      c.lb = __builtin_amdgcn_readfirstlane((c.t * kDecodeTile) / a.bs);
+      c.lb = (c.t * kDecodeTile) / a.bs;
       c.koff = c.t * kDecodeTile - c.lb * a.bs;
       return;
     }
     base = __builtin_amdgcn_readlane(incl, 63);
   }
   // Unreachable for s < T; an in-bounds cursor at row 0 keeps every access valid.
-  ch = load_chunk(a, cu_q, cu_k, 0);
-  set_row(a, cu_q, cu_k, c, ch, 0);
-  c.t = c.lb = c.koff = 0;
+  c.b = 0;
+  c.q0 = __builtin_amdgcn_readlane(r0.q[0], 0);
+  c.K = 0;
   c.n = 1;
+  c.t = c.lb = c.koff = 0;
   first = 0;
 }
 
@@ -465,11 +528,14 @@ __device__ __forceinline__ int tile_block(const DecodeArgs& a, const int32_t* __
 template <int KV>
 __device__ __forceinline__ void load_q(bf16x8 (&qop)[4], const DecodeArgs& a, int q0, int h, int col, int grp) {
   const bool use = col < a.g;
-  const uint16_t* qp = a.q + (int64_t)q0 * a.q_ts + (int64_t)(h * a.g + (use ? col : 0)) * a.q_hs +
-                       kKGroupStride<KV> * grp;
+  // Row base of the group's first head plus a 32-bit lane offset (head
+  // strides are below 2^26 elements, so (g - 1) heads fit).
+  const char* qb = (const char*)(a.q + (int64_t)q0 * a.q_ts + (int64_t)h * a.g * a.q_hs);
+  const uint32_t lo =
+      lane_off(((uint32_t)(use ? col : 0) * (uint32_t)a.q_hs + kKGroupStride<KV> * grp) * 2u);
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
-    const u32x4 x = *reinterpret_cast<const u32x4*>(qp + kKStepStride<KV> * s);
+    const u32x4 x = *reinterpret_cast<const u32x4*>(qb + lo + kKStepStride<KV> * s * 2);
     qop[s] = __builtin_bit_cast(bf16x8, use ? x : u32x4{0, 0, 0, 0});
   }
 }
@@ -483,36 +549,64 @@ __device__ __forceinline__ void finish_segment(const DecodeArgs& a, const Cursor
   if (col >= a.g) return;
   if (whole) {
     const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
-    uint16_t* op = a.out + (int64_t)c.q0 * a.out_ts + (int64_t)(h * a.g + col) * a.out_hs + 32 * grp;
+    // Row base of the group's first head plus a 32-bit lane offset, as in load_q.
+    char* ob = (char*)(a.out + (int64_t)c.q0 * a.out_ts + (int64_t)h * a.g * a.out_hs);
+    const uint32_t lo = lane_off(((uint32_t)col * (uint32_t)a.out_hs + 32u * grp) * 2u);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       u32x4 v;
 #pragma unroll
       for (int m = 0; m < 4; ++m) v[m] = pack_bf16x2(o[2 * m][r] * inv, o[2 * m + 1][r] * inv);
-      *reinterpret_cast<u32x4*>(op + 8 * r) = v;
+      *reinterpret_cast<u32x4*>(ob + lo + 16 * r) = v;
     }
   } else {
-    const int64_t base = ((int64_t)w * 2 + slot) * a.g + col;
-    float* op = a.ws_o + base * kHeadDim + 32 * grp;
+    const int64_t base = ((int64_t)w * 2 + slot) * a.g;  // partial row of head 0 of the group
+    char* ob = (char*)(a.ws_o + base * kHeadDim);
+    const uint32_t lo = lane_off(((uint32_t)col * kHeadDim + 32u * grp) * 4u);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      *reinterpret_cast<f32x4*>(op + 8 * r) = f32x4{o[0][r], o[1][r], o[2][r], o[3][r]};
-      *reinterpret_cast<f32x4*>(op + 8 * r + 4) = f32x4{o[4][r], o[5][r], o[6][r], o[7][r]};
+      *reinterpret_cast<f32x4*>(ob + lo + 32 * r) = f32x4{o[0][r], o[1][r], o[2][r], o[3][r]};
+      *reinterpret_cast<f32x4*>(ob + lo + 32 * r + 16) = f32x4{o[4][r], o[5][r], o[6][r], o[7][r]};
     }
-    if (grp == 0) *reinterpret_cast<f32x2*>(a.ws_ml + base * 2) = f32x2{m_run, l_run};
+    if (grp == 0)
+      *reinterpret_cast<f32x2*>((char*)(a.ws_ml + base * 2) + lane_off((uint32_t)col * 8u)) =
+          f32x2{m_run, l_run};
   }
 }
 
-// One decode wave (kv head h of group k): the tiles [floor(k T / Kw),
-// floor((k + 1) T / Kw)) of the batch, streamed one by one.  Cursor c is the
-// tile being computed, n1 the next one (its loads are in flight during c's
-// compute) and n2 the one after (its block id is fetched during c's
-// compute).  Loads are issued unconditionally (past the wave's last tile the
-// cursors stop advancing, so the surplus loads re-read the last tile) and the
-// two-tile ring is unrolled so every buffer index is a compile-time
-// constant.  The block table is read through a restrict-qualified pointer, so
-// its entries are scalar loads whose waits never wait for the wave's vector
-// loads.
+// Depth D of a decode wave's tile ring: the oldest tile is computed while
+// the loads of the D - 1 after it are in flight.  D = 2 for every cache: a
+// code tile carries half a bf16 tile's bytes, yet a third code tile in
+// flight measured no faster (the stream is bound by HBM throughput, not by
+// the bytes a wave keeps in flight).
+#ifndef NVS_DECODE_RING_BF16
+#define NVS_DECODE_RING_BF16 2
+#endif
+#ifndef NVS_DECODE_RING_CODES
+#define NVS_DECODE_RING_CODES 2
+#endif
+template <int KV>
+constexpr int kDecodeRing = (KV == NVS_DTYPE_BF16) ? NVS_DECODE_RING_BF16 : NVS_DECODE_RING_CODES;
+
+// Decode ranges: Kw groups of Hkv waves (one per kv head) share the T tiles,
+// group k taking [floor(k T / Kw), floor((k + 1) T / Kw)); Kw = min(launched
+// groups, T / kDecodeMinUnits), at least 1.
+__device__ __forceinline__ int decode_groups(int T, int G) {
+  return T > 0 ? min(G, max(1, T / kDecodeMinUnits)) : 0;
+}
+
+__device__ __forceinline__ int group_start(int T, int Kw, int k) { return (int)((int64_t)k * T / Kw); }
+
+// One decode wave (kv head h of group k): tiles [s0, s0 + left) of the
+// stream, streamed one by one, partials at index w.  Cursor n[0] is
+// the tile being computed, n[1] .. n[D - 1] the next ones (their loads are in
+// flight during n[0]'s compute) and n[D] the one after (its block id is
+// fetched during n[0]'s compute), D = kDecodeRing.  Loads are issued
+// unconditionally (past the wave's last tile the cursors stop advancing, so
+// the surplus loads re-read the last tile) and the ring is unrolled so every
+// buffer index is a compile-time constant.  The block table is read through
+// a restrict-qualified pointer, so its entries are scalar loads whose waits
+// never wait for the wave's vector loads.
 template <int KV>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kDecodeWavesPerEU)))
 void paged_decode_kernel(DecodeArgs a, const int32_t* __restrict__ bt, const int32_t* __restrict__ cu_q,
@@ -526,21 +620,22 @@ void paged_decode_kernel(DecodeArgs a, const int32_t* __restrict__ bt, const int
   const int w = k * a.Hkv + h;  // partial slot index
   const int lane = threadIdx.x;
 
-  const int T = decode_tiles(a, cu_q, cu_k);
-  const int Kw = T > 0 ? min(G, max(1, T / kDecodeMinUnits)) : 0;
+  ScanRound r0;
+  const int T = decode_tiles(a, cu_q, cu_k, r0);
+  const int Kw = decode_groups(T, G);
   if (k >= Kw) return;
-  const int s0 = (int)((int64_t)k * T / Kw);
-  const int left = (int)((int64_t)(k + 1) * T / Kw) - s0;  // >= 1 (Kw <= T)
+  const int s0 = group_start(T, Kw, k);
+  const int left = group_start(T, Kw, k + 1) - s0;  // >= 1 (Kw <= T)
 
   const int col = lane & 15, grp = lane >> 4;
   const LaneOffsets lo = lane_offsets<KV>(a.Hkv, col, grp);
 
+  constexpr int D = kDecodeRing<KV>;
   // Cursors.
-  Cursor c;
+  Cursor n[D + 1];
   {
-    Chunk ch;
     int first;
-    locate_tile(a, cu_q, cu_k, s0, ch, c, first);
+    locate_tile(a, cu_q, cu_k, s0, r0, n[0], first);
   }
   auto advance = [&](Cursor& x) {
     if (++x.t == x.n) {
@@ -550,29 +645,33 @@ void paged_decode_kernel(DecodeArgs a, const int32_t* __restrict__ bt, const int
       ++x.lb;
     }
   };
-  Cursor n1 = c;
-  if (left > 1) advance(n1);
-  Cursor n2 = n1;
-  if (left > 2) advance(n2);
+#pragma unroll
+  for (int j = 1; j <= D; ++j) {
+    n[j] = n[j - 1];
+    if (left > j) advance(n[j]);
+  }
 
   bf16x8 qop[4];
-  load_q<KV>(qop, a, c.q0, h, col, grp);
+  load_q<KV>(qop, a, n[0].q0, h, col, grp);
   f32x4 o[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) o[j] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.0f;
-  int seg_t0 = c.t;  // first tile of the current segment
-  int slot = 0;      // partial slot of the current segment (0: the wave's first)
+  int seg_t0 = n[0].t;  // first tile of the current segment
+  int slot = 0;         // partial slot of the current segment (0: the item's first)
 
-  DecodeTile<KV> r0, r1;
-  decode_load<KV>(r0, a, lo, tile_block(a, bt, c), c.koff, h);
-  int blk1 = tile_block(a, bt, n1);
+  DecodeTile<KV> r[D];
+#pragma unroll
+  for (int j = 0; j < D - 1; ++j) decode_load<KV>(r[j], a, lo, tile_block(a, bt, n[j]), n[j].koff, h);
+  int blk_last = tile_block(a, bt, n[D - 1]);
 
-  // Tile i (cursor c) from ring slot cur; the loads of tile i + 1 go to nxt_t.
+  // Tile i (cursor n[0]) from ring slot cur; the loads of tile i + D - 1 go
+  // to slot nxt_t.
   auto step = [&](DecodeTile<KV>& cur, DecodeTile<KV>& nxt_t, int i) {
-    decode_load<KV>(nxt_t, a, lo, blk1, n1.koff, h);
-    const int blk2 = tile_block(a, bt, n2);
+    decode_load<KV>(nxt_t, a, lo, blk_last, n[D - 1].koff, h);
+    const int blk_next = tile_block(a, bt, n[D]);
     __builtin_amdgcn_sched_barrier(0);
+    const Cursor& c = n[0];
     if (!cur.has) zero_tile(cur);
     const int kt = c.t * kDecodeTile;
     if (kt + kDecodeTile > c.K)  // the row's last, partial tile
@@ -584,68 +683,74 @@ void paged_decode_kernel(DecodeArgs a, const int32_t* __restrict__ bt, const int
       float l = l_run + shfl_xor(l_run, 16);
       l += shfl_xor(l, 32);
       finish_segment(a, c, h, seg_t0 == 0 && c.t == c.n - 1, w, slot, o, m_run, l, col, grp);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) o[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      // The next tile clears o: with m_run = -inf its rescale always runs,
+      // with alpha = 2^-inf = 0 (its first key is visible, so its max is
+      // finite).  Not writing o here keeps it in one register set.
       m_run = -INFINITY;
       l_run = 0.0f;
       seg_t0 = 0;
       slot = 1;
       // The next segment's q (tile i + 1 starts it); its wait falls at tile
       // i + 1's compute, which waits for that tile's loads anyway.
-      if (i + 1 < left) load_q<KV>(qop, a, n1.q0, h, col, grp);
+      if (i + 1 < left) load_q<KV>(qop, a, n[1].q0, h, col, grp);
     }
-    c = n1;
-    n1 = n2;
-    if (i + 3 < left) advance(n2);
-    blk1 = blk2;
+#pragma unroll
+    for (int j = 0; j < D; ++j) n[j] = n[j + 1];
+    if (i + D + 1 < left) advance(n[D]);
+    blk_last = blk_next;
   };
-  for (int i = 0; i < left; i += 2) {
-    step(r0, r1, i);
-    if (i + 1 >= left) break;
-    step(r1, r0, i + 1);
+  for (int i = 0; i < left; i += D) {
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      if (i + j >= left) break;
+      step(r[j], r[(j + D - 1) % D], i + j);
+    }
   }
 }
 
 // Log-sum-exp merge of the rows split across groups (and the zeroing of
-// decode rows without a visible key).  Wave k Hkv + h owns
-// kv head h of the row that crosses the boundary after group k if that row
-// starts inside group k's range; its partials sit in wave k Hkv + h (slot 0
-// if the row is the group's first segment, else slot 1) and in waves
-// x Hkv + h for groups x = k + 1 .. k_last (slot 0).  Lane l serves
-// head 4 p + l / 16 of the group (pass p) and head_dim elements 8 (l % 16) ..
-// + 7; one pass over the partials keeps a running max, sum and output, with
-// the loads of four partials in flight at a time.
+// decode rows without a visible key).  Wave k Hkv + h owns kv head h of the
+// row that crosses the boundary after group k if that row starts inside
+// group k's range; its partials sit in wave k Hkv + h (slot 0 if the row is
+// the group's first segment, else slot 1) and in waves x Hkv + h for groups
+// x = k + 1 .. k_last (slot 0).  Lane l serves head 4 p + l / 16 of the
+// group (pass p) and head_dim elements 8 (l % 16) .. + 7; one pass over the
+// partials keeps a running max, sum and output, with the loads of four
+// partials in flight at a time.
 __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a, int groups, const int32_t* __restrict__ cu_q,
                                                          const int32_t* __restrict__ cu_k) {
   const int k = blockIdx.x / a.Hkv, h = blockIdx.x - k * a.Hkv;
   const int lane = threadIdx.x;
   // Tiles, and the zeroing of decode rows without a visible key (row b by
   // merge wave b % gridDim.x).
+  const ScanRound r0 = load_round(a, cu_q, cu_k, 0);
   int T = 0;
-  for (int c0 = 0; c0 < a.B; c0 += 64) {
-    const int b = c0 + lane;
-    RowInfo ri = {false, 0, 0};
-    if (b < a.B) ri = row_info(a, cu_q, cu_k, b);
-    T += wave_sum_i(row_tiles(ri));
-    uint64_t z = __ballot(ri.dec && ri.K <= 0 && b % (int)gridDim.x == (int)blockIdx.x);
-    while (z) {
-      const int li = __builtin_ctzll(z);
-      z &= z - 1;
-      const int q0 = __builtin_amdgcn_readlane(ri.q0, li);
-      for (int i = lane; i < a.Hq * (kHeadDim / 8); i += 64) {
-        const int hq = i / (kHeadDim / 8), d = 8 * (i % (kHeadDim / 8));
-        *reinterpret_cast<u32x4*>(a.out + (int64_t)q0 * a.out_ts + (int64_t)hq * a.out_hs + d) = u32x4{0, 0, 0, 0};
+  for (int c0 = 0; c0 < a.B; c0 += kScanSpan) {
+    const ScanRound rd = c0 == 0 ? r0 : load_round(a, cu_q, cu_k, c0);
+    T += wave_sum_i(lane_tiles(a, rd));
+#pragma unroll
+    for (int i = 0; i < kScanRows; ++i) {
+      const int b = rd.c0 + kScanRows * lane + i;
+      const bool dec = rd.q[i + 1] - rd.q[i] == 1 && rd.q[i] >= 0 && (int64_t)rd.q[i + 1] <= a.T;
+      uint64_t z = __ballot(b < a.B && dec && rd.k[i + 1] - rd.k[i] <= 0 && b % (int)gridDim.x == (int)blockIdx.x);
+      while (z) {
+        const int li = __builtin_ctzll(z);
+        z &= z - 1;
+        const int q0 = __builtin_amdgcn_readlane(rd.q[i], li);
+        for (int x = lane; x < a.Hq * (kHeadDim / 8); x += 64) {
+          const int hq = x / (kHeadDim / 8), d = 8 * (x % (kHeadDim / 8));
+          *reinterpret_cast<u32x4*>(a.out + (int64_t)q0 * a.out_ts + (int64_t)hq * a.out_hs + d) = u32x4{0, 0, 0, 0};
+        }
       }
     }
   }
-  const int Kw = T > 0 ? min(groups, max(1, T / kDecodeMinUnits)) : 0;
+  const int Kw = decode_groups(T, groups);
   if (k + 1 >= Kw) return;
-  Chunk ch;
   Cursor r;
   int first;  // the first tile of the row at the boundary after group k
-  locate_tile(a, cu_q, cu_k, (int)((int64_t)(k + 1) * T / Kw), ch, r, first);
+  locate_tile(a, cu_q, cu_k, group_start(T, Kw, k + 1), r0, r, first);
   if (r.t == 0) return;  // the boundary falls between rows
-  const int sk = (int)((int64_t)k * T / Kw);
+  const int sk = group_start(T, Kw, k);
   if (first < sk) return;  // started in an earlier group, which merges it
   const int last = first + r.n - 1;
   const int k_last = (int)(((int64_t)(last + 1) * Kw - 1) / T);
