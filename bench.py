@@ -81,7 +81,45 @@ def bench_decode(steps, warmup):
         "tokens_per_s": wl.num_seqs / (ms_step / 1e3),
     }
     log(f"decode_8b: {ms_step:.3f} ms/step, attention {ms_attn:.3f} ms -> {res['gbs_attention']:.0f} GB/s")
+    res["graph_ms_per_step"] = graph_step_ms(wl, steps, warmup)
+    log(f"decode_8b: {res['graph_ms_per_step']:.3f} ms/step replayed from a HIP graph")
+    # A launch-bound step: the 8-sequence decode batch, eager against replayed.
+    small = W.decode_small("cuda")
+    wall, ms_small = timed_steps(step(small), steps, warmup)
+    res["small_step"] = {
+        "workload": "decode_small: 16q/8kv heads, D128, 8 seqs ctx U[128,1024], seed 0; step = store + decode",
+        "eager_ms_per_step": ms_small,
+        "eager_wall_ms_per_step": wall,
+        "graph_ms_per_step": graph_step_ms(small, steps, warmup),
+    }
+    log(f"decode_small: eager {ms_small * 1e3:.1f} us/step (wall {wall * 1e3:.1f}), "
+        f"graph {res['small_step']['graph_ms_per_step'] * 1e3:.1f} us/step")
+    del small
     return wl, res
+
+
+def graph_step_ms(wl, steps, warmup):
+    """ms per decode step (store + attention) replayed from a captured HIP graph."""
+    from nanovllm_self_amd.layers.attention import reserve_attention_workspace
+
+    attn, ctx = wl.attn, wl.context
+    reserve_attention_workspace(wl.num_seqs, int(ctx.max_seqlen_q), int(ctx.max_seqlen_k), attn.num_heads,
+                                wl.q.device, num_kv_heads=attn.num_kv_heads)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        attn.forward(wl.q, wl.k, wl.v, ctx)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    attn.in_cuda_graph_capture = True
+    try:
+        with torch.cuda.graph(graph):
+            attn.forward(wl.q, wl.k, wl.v, ctx)
+    finally:
+        attn.in_cuda_graph_capture = False
+    _, ms = timed_steps(graph.replay, steps, warmup)
+    return ms
 
 
 def bench_prefill(steps, warmup):

@@ -281,6 +281,46 @@ def test_more_rows_than_one_plan_chunk(device):
     _check(wl, ids, "1100-row batch")
 
 
+@pytest.mark.parametrize("kv", ["bf16", "fp8"])
+def test_decode_step_graph_replay(device, kv):
+    """The decode step (store + attention) captured in a HIP graph: every
+    replay, with eager calls and synchronisations between replays, equals the
+    eager result bit for bit (the same kernels on the same inputs; the store
+    rewrites the same token)."""
+    from nanovllm_self_amd.layers.attention import reserve_attention_workspace
+
+    say(f"graph replay decode_small/{kv}")
+    wl = W.decode_small(device, kv=kv)
+    attn, ctx = wl.attn, wl.context
+    reserve_attention_workspace(wl.num_seqs, 1, int(ctx.max_seqlen_k), attn.num_heads, device,
+                                num_kv_heads=attn.num_kv_heads)
+    eager = attn.forward(wl.q, wl.k, wl.v, ctx).clone()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            attn.forward(wl.q, wl.k, wl.v, ctx)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    attn.in_cuda_graph_capture = True
+    try:
+        with torch.cuda.graph(graph):
+            out = attn.forward(wl.q, wl.k, wl.v, ctx)
+    finally:
+        attn.in_cuda_graph_capture = False
+    for r in range(4):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {r} differs from the eager step"
+        again = attn.forward(wl.q, wl.k, wl.v, ctx)
+        torch.cuda.synchronize()
+        assert torch.equal(again, eager), f"eager step after replay {r} differs"
+    ref, rows = oracle_paged(wl, list(range(wl.num_seqs)))
+    compare(bf16_to_np(out)[rows], ref, kv != "bf16", f"graph replay {kv}")
+
+
 # ---------------------------------------------------------------- API
 def test_forward_profile_and_decode_entry(device):
     say("profile + decode_flashattn")
