@@ -14,7 +14,7 @@ decode tokens/s (256 sequences, ctx U[1024, 4096], fp8 / int8 / bf16, seed
 4), the dominant kernel's roofline fraction (HIP events on the launch
 stream) and the CPU eager restatement timed on the host cores.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only decode|prefill|quant|mixed]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only decode|prefill|quant|mixed|prep]
 """
 from __future__ import annotations
 
@@ -169,6 +169,66 @@ def bench_quant(steps, warmup):
     return out
 
 
+def bench_prep(steps, warmup):
+    """The fused pre-attention step (q/k RMSNorm + rotary embedding + KV
+    store, one launch) against the same work as separate eager ops (the
+    reference's RMSNorm and rotary formulas in torch, then the store
+    kernel), at the decode_8b and prefill_8b token counts."""
+    from nanovllm_self_amd import PagedAttention
+    from nanovllm_self_amd.kv_cache import KVCacheConfig, allocate_kv_cache, bind_kv_cache
+
+    Hq, Hkv, D, bs, NB, max_pos = 32, 8, 128, 256, 1024, 40960
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev).manual_seed(5)
+    inv_freq = 1.0 / (1e6 ** (torch.arange(0, D, 2, dtype=torch.float, device=dev) / D))
+    freqs = torch.einsum("i,j->ij", torch.arange(max_pos, device=dev).float(), inv_freq)
+    table = torch.cat((freqs.cos(), freqs.sin()), dim=1).unsqueeze(1)  # [max_pos, 1, D]
+    out = {"workload": "Qwen3-8B heads (32q/8kv, D128), bf16 KV, block 256; q/k/v random, positions "
+                       "random in [0, 40960), every token stored"}
+
+    def rms(x, w, eps=1e-6):  # RMSNorm.py:11-18
+        x32 = x.float()
+        return (w.float() * x32 / torch.sqrt(x32.pow(2).mean(-1, keepdim=True) + eps)).to(x.dtype)
+
+    def rope(x, cos, sin):  # RoPE.py:5-25
+        x1, x2 = torch.chunk(x.float(), 2, dim=-1)
+        return torch.cat((x1 * cos - x2 * sin, x2 * cos + x1 * sin), dim=-1).to(x.dtype)
+
+    for name, T in (("decode_8b", 64), ("prefill_8b", 36864)):
+        cfg = KVCacheConfig(dtype=torch.bfloat16, kv_cache_dtype=torch.bfloat16,
+                            attention_compute_dtype=torch.bfloat16, block_size=bs, num_blocks=NB * (1 + T // 4096))
+        attn = PagedAttention(Hq, Hkv, D, dtype=torch.bfloat16)
+        kv_cache, scales = allocate_kv_cache(1, Hkv, D, cfg, dev)
+        bind_kv_cache([attn], kv_cache, scales, cfg)
+        q = torch.randn(T, Hq, D, generator=g, device=dev).to(torch.bfloat16)
+        k = torch.randn(T, Hkv, D, generator=g, device=dev).to(torch.bfloat16)
+        v = torch.randn(T, Hkv, D, generator=g, device=dev).to(torch.bfloat16)
+        w = (1 + 0.1 * torch.randn(D, generator=g, device=dev)).to(torch.bfloat16)
+        pos = torch.randint(0, max_pos, (T,), generator=g, device=dev)
+        slots = torch.randperm(cfg.num_blocks * bs, generator=g, device=dev)[:T].to(torch.int32)
+
+        def fused():
+            attn.qk_norm_rope_store(q, k, v, pos, w, w, 1e-6, table, slots)
+
+        def unfused():
+            cs = table[pos]
+            cos, sin = cs.chunk(2, dim=-1)
+            qr, kr = rope(rms(q, w), cos, sin), rope(rms(k, w), cos, sin)
+            attn.store_kv_cache_torch(kr, v, slots)
+            return qr
+
+        nbytes = T * (2 * D * (2 * Hq + 4 * Hkv) + 4 * D)
+        _, ms_f = timed_steps(fused, steps, warmup)
+        _, ms_u = timed_steps(unfused, steps, warmup)
+        out[name] = {"tokens": T, "bytes": nbytes, "ms_fused": ms_f, "gbs_fused": nbytes / ms_f / 1e6,
+                     "ms_unfused": ms_u, "speedup": ms_u / ms_f}
+        log(f"prep {name}: fused {ms_f * 1e3:.1f} us ({nbytes / ms_f / 1e6:.0f} GB/s), "
+            f"eager ops {ms_u * 1e3:.1f} us")
+        del attn, kv_cache, q, k, v
+        torch.cuda.empty_cache()
+    return out
+
+
 def bench_mixed(steps, warmup):
     from nanovllm_self_amd import workloads as W
 
@@ -266,7 +326,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", choices=["decode", "prefill", "quant", "mixed"], default=None)
+    ap.add_argument("--only", choices=["decode", "prefill", "quant", "mixed", "prep"], default=None)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--calib-copy", action="store_true",
                     help="only run a 1 GiB device copy (for scaling PMC byte counters)")
@@ -295,6 +355,9 @@ def main():
         return
     if args.only == "mixed":
         print(json.dumps(bench_mixed(steps, warmup)))
+        return
+    if args.only == "prep":
+        print(json.dumps(bench_prep(steps, warmup)))
         return
 
     wl, dec = bench_decode(steps, warmup)
@@ -338,6 +401,7 @@ def main():
         line["prefill_8b"] = bench_prefill(max(5, steps // 4), 2)
         line["decode_quant"] = bench_quant(steps, warmup)
         line["mixed_32b"] = bench_mixed(max(5, steps // 4), 2)
+        line["qk_prep"] = bench_prep(steps, warmup)
     print(json.dumps(line))
 
 

@@ -92,6 +92,42 @@ int nvs_store_kvcache(const void* k, const void* v, int src_dtype,
                       int head_dim, void* stream);
 
 /*
+ * Fused pre-attention step of a Qwen3 attention layer: per-head RMSNorm of q
+ * and k, rotary embedding of both, and the KV-cache write of the rotated k and
+ * of v.  Replaces the sequence q_norm(q); k_norm(k); rotary_embedding(
+ * positions, q, k); write_kv_cache(k, v, slot_mapping) of the reference
+ * (nanovllm/models/qwen3.py:100-104 and :118 via attention.py:500-546, with
+ * layers/RMSNorm.py:11-18, layers/RoPE.py:5-25 and 60-74,
+ * attention.py:139-189).
+ *   q [num_tokens, num_heads, head_dim], k, v [num_tokens, num_kv_heads,
+ *     head_dim]: BF16, strides (tok, head) in elements.
+ *   positions       [num_tokens] int64, clamped into [0, max_position).
+ *   q/k_norm_weight [head_dim] BF16; eps the layers' rms_norm_eps.
+ *   cos_sin_cache   [max_position, head_dim] fp32 (the rotary layer's buffer:
+ *                   cos of the head_dim / 2 frequencies, then their sin).
+ *   Per (token, head), in fp32 with every product and sum rounded on its own:
+ *     rms = sqrt(mean(x^2) + eps); n = bf16((w * x) / rms);
+ *     y1 = n1 cos - n2 sin, y2 = n2 cos + n1 sin over the halves n1, n2 of n;
+ *     out = bf16(y1 ++ y2).
+ *   q_out receives the rotated q; k_out (may be NULL) the rotated k; the
+ *   cache write of the rotated k and of v follows nvs_store_kvcache (same
+ *   slot rule, casts and quantisation).  head_dim must be 128.
+ */
+int nvs_qk_norm_rope_store(const void* q, int64_t q_tok_stride, int64_t q_head_stride,
+                           const void* k, int64_t k_tok_stride, int64_t k_head_stride,
+                           const void* v, int64_t v_tok_stride, int64_t v_head_stride,
+                           const int64_t* positions, int64_t num_tokens,
+                           const void* q_norm_weight, const void* k_norm_weight, float eps,
+                           const float* cos_sin_cache, int64_t max_position,
+                           const int32_t* slot_mapping, void* k_cache, void* v_cache,
+                           int cache_dtype, float* k_scale, float* v_scale,
+                           int64_t num_blocks, int block_size, int num_heads,
+                           int num_kv_heads, int head_dim,
+                           void* q_out, int64_t q_out_tok_stride, int64_t q_out_head_stride,
+                           void* k_out, int64_t k_out_tok_stride, int64_t k_out_head_stride,
+                           void* stream);
+
+/*
  * Per-token, per-head quantisation of a [num_tokens, num_heads, head_dim]
  * tensor into contiguous codes (same shape) and fp32 scales
  * [num_tokens, num_heads].  Replaces PagedAttention.quantize_int8_per_token

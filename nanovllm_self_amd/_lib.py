@@ -60,6 +60,19 @@ SIGNATURES = {
             _P, _L, _P,  # workspace, bytes, stream
         ],
     ),
+    "nvs_qk_norm_rope_store": (
+        _I,
+        [
+            _P, _L, _L, _P, _L, _L, _P, _L, _L,  # q, k, v
+            _P, _L,  # positions, num_tokens
+            _P, _P, _F,  # q_norm weight, k_norm weight, eps
+            _P, _L,  # cos_sin_cache, max_position
+            _P, _P, _P, _I, _P, _P, _L, _I,  # slots, caches, dtype, scales, blocks, block_size
+            _I, _I, _I,  # heads, kv heads, head_dim
+            _P, _L, _L, _P, _L, _L,  # q_out, k_out
+            _P,  # stream
+        ],
+    ),
     "nvs_varlen_attention": (
         _I,
         [

@@ -1,0 +1,259 @@
+// Fused pre-attention step of a Qwen3 attention layer for gfx950: per-head
+// RMSNorm of q and k, rotary embedding of both, and the KV-cache write of
+// the rotated k and of v (quantised for int8 / fp8 caches).
+//
+// Reference semantics (nanovllm/models/qwen3.py:100-104 and the layers it
+// calls):
+//   RMSNorm (layers/RMSNorm.py:11-18), per (token, head) in fp32:
+//     rms = sqrt(mean(x^2) + eps);  y = bf16((w * x) / rms)
+//   rotary embedding (layers/RoPE.py:5-25, 60-74), cos/sin from the model's
+//   fp32 cos_sin_cache [max_position, 1, 2 * (D / 2)] at the token's position:
+//     x1, x2 = first and second half of the normalised head (as fp32)
+//     y1 = x1 cos - x2 sin;  y2 = x2 cos + x1 sin;  out = bf16(cat(y1, y2))
+//   KV write (layers/attention.py:139-189): as nvs_store_kvcache, from the
+//   rotated bf16 k and the raw v.
+// Each product and sum is rounded on its own (no fused multiply-add), as the
+// eager torch ops compute them.
+//
+// Work: 16 lanes per (token, unit) row, units = Hq query heads, then Hkv key
+// heads, then Hkv value heads (four rows per wave); lane j holds elements
+// 8 j .. 8 j + 7 of its head (head_dim 128) as one 16-byte load, its rotary
+// partners (elements +-64) sit in lane j ^ 8, and the norm's sum is a
+// butterfly over the row's 16 lanes.
+#include <algorithm>
+
+#include "nvs_common.h"
+#include "store_common.h"
+
+namespace nvs {
+
+namespace {
+
+constexpr int kPrepD = 128;
+constexpr int kRowLanes = 16;  // lanes per head row, 8 elements each
+constexpr int kPrepThreads = 256;
+
+struct PrepArgs {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  int64_t q_ts, q_hs, k_ts, k_hs, v_ts, v_hs;
+  const int64_t* pos;
+  int64_t T;
+  const uint16_t* qw;
+  const uint16_t* kw;
+  float eps;
+  const float* cs;  // [max_pos, 128]: cos at 0..63, sin at 64..127
+  int64_t max_pos;
+  const int32_t* slots;
+  int64_t total_slots;
+  void* kc;
+  void* vc;
+  float* ks;
+  float* vs;
+  int Hq, Hkv;
+  uint16_t* qo;
+  int64_t qo_ts, qo_hs;
+  uint16_t* ko;  // may be null
+  int64_t ko_ts, ko_hs;
+};
+
+__device__ __forceinline__ float bf16r(float x) { return bf16_bits_to_f32(f32_to_bf16_bits(x)); }
+
+// Products and sums rounded one by one: with contraction off the compiler
+// cannot fuse x * c - y * s into a multiply-add.  (Division is correctly
+// rounded in this build's float model.)
+__device__ __forceinline__ float mul_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a * b;
+}
+__device__ __forceinline__ float sub_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a - b;
+}
+__device__ __forceinline__ float add_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a + b;
+}
+
+// Lane j ^ m of the lane's 16-lane row, for m = 1, 2, 4, 8, as DPP moves
+// (VALU, no trip through the LDS crossbar): quad_perm for 1 and 2,
+// row_half_mirror (j ^ 7) then quad_perm j ^ 3 for 4, and a rotation of the
+// row by 8 for 8.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+template <int M>
+__device__ __forceinline__ float row_xor(float v) {
+  if constexpr (M == 1) return dpp<0xB1>(v);  // quad_perm(1, 0, 3, 2)
+  if constexpr (M == 2) return dpp<0x4E>(v);  // quad_perm(2, 3, 0, 1)
+  if constexpr (M == 4) return dpp<0x1B>(dpp<0x141>(v));  // half mirror, then quad_perm(3, 2, 1, 0)
+  return dpp<0x128>(v);  // row_ror:8
+}
+
+// Sum over the 16 lanes of a head row: a butterfly, lane partners j ^ 1,
+// j ^ 2, j ^ 4, j ^ 8.
+__device__ __forceinline__ float row_sum16(float v) {
+  v = add_rn(v, row_xor<1>(v));
+  v = add_rn(v, row_xor<2>(v));
+  v = add_rn(v, row_xor<4>(v));
+  return add_rn(v, row_xor<8>(v));
+}
+
+// Writes lane j's 8 elements of head row `row` of a cache of dtype DST;
+// quantised caches take the row scale from the absmax over the row's lanes.
+template <int DST>
+__device__ __forceinline__ void cache_row(void* cache, float* scales, int64_t row, const float (&x)[8],
+                                          bool write) {
+  const int j = threadIdx.x & (kRowLanes - 1);
+  const int64_t e = row * kPrepD + 8 * j;
+  if constexpr (DST == NVS_DTYPE_INT8 || DST == NVS_DTYPE_FP8_E4M3) {
+    constexpr float qmax = (DST == NVS_DTYPE_INT8) ? QuantInt8::kQmax : QuantFp8::kQmax;
+    const float sc = quant_scale(row_absmax(x, kRowLanes), qmax);
+    if (write) {
+      *reinterpret_cast<u32x2*>((uint8_t*)cache + e) = quant8<DST>(x, sc);
+      if (j == 0) scales[row] = sc;
+    }
+  } else {
+    constexpr int B = (DST == NVS_DTYPE_FP32) ? 4 : 2;
+    if (write) store8_float<DST>((char*)cache + e * B, x);
+  }
+}
+
+template <int DST>
+__global__ __launch_bounds__(kPrepThreads) void qk_prep_kernel(PrepArgs a) {
+  const int U = a.Hq + 2 * a.Hkv;
+  const int64_t rows = a.T * U;
+  const int64_t unit = ((int64_t)blockIdx.x * kPrepThreads + threadIdx.x) / kRowLanes;
+  if (unit >= rows) return;  // whole rows exit together
+  const int64_t t = unit / U;
+  const int u = (int)(unit - t * U);
+  const int j = threadIdx.x & (kRowLanes - 1);
+  const int64_t slot = a.slots[t];
+  const bool ok = slot >= 0 && slot < a.total_slots;
+
+  if (u >= a.Hq + a.Hkv) {  // value head: cast / quantise into the cache
+    const int h = u - a.Hq - a.Hkv;
+    float x[8];
+    load8<NVS_DTYPE_BF16>(a.v + t * a.v_ts + (int64_t)h * a.v_hs + 8 * j, x);
+    cache_row<DST>(a.vc, a.vs, (ok ? slot : 0) * a.Hkv + h, x, ok);
+    return;
+  }
+  const bool is_q = u < a.Hq;
+  const int h = is_q ? u : u - a.Hq;
+  float x[8], w[8];
+  load8<NVS_DTYPE_BF16>(is_q ? a.q + t * a.q_ts + (int64_t)h * a.q_hs + 8 * j
+                             : a.k + t * a.k_ts + (int64_t)h * a.k_hs + 8 * j,
+                        x);
+  load8<NVS_DTYPE_BF16>((is_q ? a.qw : a.kw) + 8 * j, w);
+
+  // RMSNorm: mean of squares over the 128 elements (division by 128 is exact).
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ss = add_rn(ss, mul_rn(x[i], x[i]));
+  ss = row_sum16(ss);
+  // __builtin_sqrtf is the correctly rounded square root (HIP's __fsqrt_rn
+  // is the raw v_sqrt_f32 here, off by an ulp at times).
+  const float rms = __builtin_sqrtf(add_rn(mul_rn(ss, 1.0f / kPrepD), a.eps));
+  float n[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) n[i] = bf16r(__fdiv_rn(mul_rn(w[i], x[i]), rms));
+
+  // Rotary pairs (e, e + 64): lanes j and j ^ 8 hold the two halves.
+  int64_t p = a.pos[t];
+  p = p < 0 ? 0 : (p >= a.max_pos ? a.max_pos - 1 : p);
+  const float* cs = a.cs + p * kPrepD + 8 * (j & 7);
+  float c[8], s[8];
+  *reinterpret_cast<f32x4*>(c) = *reinterpret_cast<const f32x4*>(cs);
+  *reinterpret_cast<f32x4*>(c + 4) = *reinterpret_cast<const f32x4*>(cs + 4);
+  *reinterpret_cast<f32x4*>(s) = *reinterpret_cast<const f32x4*>(cs + 64);
+  *reinterpret_cast<f32x4*>(s + 4) = *reinterpret_cast<const f32x4*>(cs + 68);
+  const bool first = j < 8;
+  float y[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float other = row_xor<8>(n[i]);
+    // first half: y1 = x1 cos - x2 sin; second half: y2 = x2 cos + x1 sin
+    y[i] = first ? bf16r(sub_rn(mul_rn(n[i], c[i]), mul_rn(other, s[i])))
+                 : bf16r(add_rn(mul_rn(n[i], c[i]), mul_rn(other, s[i])));
+  }
+
+  if (is_q) {
+    store8_float<NVS_DTYPE_BF16>(a.qo + t * a.qo_ts + (int64_t)h * a.qo_hs + 8 * j, y);
+    return;
+  }
+  if (a.ko) store8_float<NVS_DTYPE_BF16>(a.ko + t * a.ko_ts + (int64_t)h * a.ko_hs + 8 * j, y);
+  cache_row<DST>(a.kc, a.ks, (ok ? slot : 0) * a.Hkv + h, y, ok);
+}
+
+bool is_code_dtype(int dt) { return dt == NVS_DTYPE_INT8 || dt == NVS_DTYPE_FP8_E4M3; }
+
+}  // namespace
+}  // namespace nvs
+
+using namespace nvs;
+
+extern "C" int nvs_qk_norm_rope_store(const void* q, int64_t q_tok_stride, int64_t q_head_stride,
+                                      const void* k, int64_t k_tok_stride, int64_t k_head_stride,
+                                      const void* v, int64_t v_tok_stride, int64_t v_head_stride,
+                                      const int64_t* positions, int64_t num_tokens,
+                                      const void* q_norm_weight, const void* k_norm_weight, float eps,
+                                      const float* cos_sin_cache, int64_t max_position,
+                                      const int32_t* slot_mapping, void* k_cache, void* v_cache,
+                                      int cache_dtype, float* k_scale, float* v_scale, int64_t num_blocks,
+                                      int block_size, int num_heads, int num_kv_heads, int head_dim,
+                                      void* q_out, int64_t q_out_tok_stride, int64_t q_out_head_stride,
+                                      void* k_out, int64_t k_out_tok_stride, int64_t k_out_head_stride,
+                                      void* stream) {
+  clear_error();
+  const char* who = "qk_norm_rope_store";
+  NVS_REQUIRE(num_tokens >= 0, NVS_ERR_INVALID, "%s: num_tokens < 0", who);
+  NVS_REQUIRE(head_dim == kPrepD, NVS_ERR_UNSUPPORTED, "%s: head_dim %d (this build serves 128)", who,
+              head_dim);
+  NVS_REQUIRE(num_heads > 0 && num_kv_heads > 0, NVS_ERR_INVALID, "%s: head counts must be positive", who);
+  NVS_REQUIRE(q_norm_weight && k_norm_weight && cos_sin_cache && k_cache && v_cache, NVS_ERR_INVALID,
+              "%s: null pointer argument", who);
+  // Per-token arrays may be null for an empty batch.
+  NVS_REQUIRE(num_tokens == 0 || (q && k && v && positions && slot_mapping && q_out), NVS_ERR_INVALID,
+              "%s: null pointer argument", who);
+  NVS_REQUIRE(max_position > 0, NVS_ERR_INVALID, "%s: max_position must be positive", who);
+  NVS_REQUIRE(eps >= 0.0f, NVS_ERR_INVALID, "%s: eps must be >= 0", who);
+  NVS_REQUIRE(num_blocks > 0 && block_size > 0, NVS_ERR_INVALID, "%s: empty cache", who);
+  NVS_REQUIRE(cache_dtype == NVS_DTYPE_BF16 || cache_dtype == NVS_DTYPE_FP16 || cache_dtype == NVS_DTYPE_FP32 ||
+                  is_code_dtype(cache_dtype),
+              NVS_ERR_UNSUPPORTED, "%s: cache dtype %d", who, cache_dtype);
+  NVS_REQUIRE(!is_code_dtype(cache_dtype) || (k_scale && v_scale), NVS_ERR_INVALID,
+              "%s: quantised caches need k_scale and v_scale", who);
+  NVS_REQUIRE(q_tok_stride >= 0 && q_head_stride >= 0 && k_tok_stride >= 0 && k_head_stride >= 0 &&
+                  v_tok_stride >= 0 && v_head_stride >= 0 && q_out_tok_stride >= 0 && q_out_head_stride >= 0 &&
+                  k_out_tok_stride >= 0 && k_out_head_stride >= 0,
+              NVS_ERR_INVALID, "%s: negative stride", who);
+  const int64_t units = num_tokens * (num_heads + 2 * (int64_t)num_kv_heads);
+  if (units == 0) return NVS_OK;
+  constexpr int kRowsPerBlock = kPrepThreads / kRowLanes;
+  const int64_t blocks = (units + kRowsPerBlock - 1) / kRowsPerBlock;
+  NVS_REQUIRE(blocks < (1ll << 31), NVS_ERR_INVALID, "%s: too many tokens (%lld)", who, (long long)num_tokens);
+  PrepArgs a;
+  a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v;
+  a.q_ts = q_tok_stride; a.q_hs = q_head_stride; a.k_ts = k_tok_stride; a.k_hs = k_head_stride;
+  a.v_ts = v_tok_stride; a.v_hs = v_head_stride;
+  a.pos = positions; a.T = num_tokens;
+  a.qw = (const uint16_t*)q_norm_weight; a.kw = (const uint16_t*)k_norm_weight; a.eps = eps;
+  a.cs = cos_sin_cache; a.max_pos = max_position;
+  a.slots = slot_mapping; a.total_slots = num_blocks * (int64_t)block_size;
+  a.kc = k_cache; a.vc = v_cache; a.ks = k_scale; a.vs = v_scale;
+  a.Hq = num_heads; a.Hkv = num_kv_heads;
+  a.qo = (uint16_t*)q_out; a.qo_ts = q_out_tok_stride; a.qo_hs = q_out_head_stride;
+  a.ko = (uint16_t*)k_out; a.ko_ts = k_out_tok_stride; a.ko_hs = k_out_head_stride;
+  hipStream_t s = (hipStream_t)stream;
+  dim3 grid((unsigned)blocks), block(kPrepThreads);
+  switch (cache_dtype) {
+    case NVS_DTYPE_BF16: hipLaunchKernelGGL(qk_prep_kernel<NVS_DTYPE_BF16>, grid, block, 0, s, a); break;
+    case NVS_DTYPE_FP16: hipLaunchKernelGGL(qk_prep_kernel<NVS_DTYPE_FP16>, grid, block, 0, s, a); break;
+    case NVS_DTYPE_FP32: hipLaunchKernelGGL(qk_prep_kernel<NVS_DTYPE_FP32>, grid, block, 0, s, a); break;
+    case NVS_DTYPE_INT8: hipLaunchKernelGGL(qk_prep_kernel<NVS_DTYPE_INT8>, grid, block, 0, s, a); break;
+    default: hipLaunchKernelGGL(qk_prep_kernel<NVS_DTYPE_FP8_E4M3>, grid, block, 0, s, a); break;
+  }
+  return check_launch(who);
+}

@@ -382,6 +382,79 @@ class PagedAttention(nn.Module):
     def forward(self, q, k, v, context):
         return self.forward_unified(q, k, v, context)
 
+    # ------------------------------------------------ fused pre-attention step
+    def qk_norm_rope_store(self, q, k, v, positions, q_norm_weight, k_norm_weight, eps, cos_sin_cache,
+                           slot_mapping, want_k=False):
+        """One launch for q_norm(q), k_norm(k), rotary_embedding(positions, q, k)
+        and write_kv_cache(k, v, slot_mapping) (qwen3.py:100-104, RMSNorm.py:11-18,
+        RoPE.py:5-25 and 60-74, attention.py:139-189).  q [T, Hq, 128], k, v
+        [T, Hkv, 128] bf16; cos_sin_cache the rotary layer's fp32 buffer
+        [max_position, 1, 128]; positions outside the table are clamped.
+        Returns (rotated q, rotated k or None)."""
+        kc, vc = self.k_cache, self.v_cache
+        if kc is None or vc is None:
+            raise RuntimeError("k_cache / v_cache are not bound")
+        for t, name in ((q, "q"), (k, "k"), (v, "v"), (positions, "positions"), (cos_sin_cache, "cos_sin_cache"),
+                        (slot_mapping, "slot_mapping"), (kc, "k_cache")):
+            _need_device(t, name)
+        for t, name in ((q, "q"), (k, "k"), (v, "v")):
+            if t.dtype != torch.bfloat16 or t.stride(-1) != 1:
+                raise RuntimeError(f"{name} must be bf16 with a contiguous head_dim")
+        mode = self.kv_cache_quant_mode
+        quant = mode in _QUANT_DTYPE
+        if quant and kc.dtype != _QUANT_DTYPE[mode]:
+            raise RuntimeError(f"{mode} KV cache must be {_QUANT_DTYPE[mode]}, got {kc.dtype}")
+        if not quant and kc.dtype in (torch.int8, torch.float8_e4m3fn):
+            raise RuntimeError(f"cache dtype {kc.dtype} needs a quantised kv_cache_quant_mode")
+        if not kc.is_contiguous() or not vc.is_contiguous():
+            raise RuntimeError("k_cache / v_cache must be contiguous [num_blocks, block_size, Hkv, D]")
+        T, Hq, D = q.shape
+        Hkv = k.shape[1]
+        table = cos_sin_cache.reshape(-1, D)
+        if table.dtype != torch.float32 or not table.is_contiguous():
+            table = table.to(torch.float32).contiguous()
+        pos = positions.reshape(-1)
+        if pos.dtype != torch.int64 or not pos.is_contiguous():
+            pos = pos.to(torch.int64).contiguous()
+        slots = slot_mapping
+        if slots.dtype != torch.int32 or not slots.is_contiguous():
+            slots = slots.to(torch.int32).contiguous()
+        qw = q_norm_weight.to(torch.bfloat16).contiguous()
+        kw = k_norm_weight.to(torch.bfloat16).contiguous()
+        q_out = torch.empty(T, Hq, D, dtype=torch.bfloat16, device=q.device)
+        k_out = torch.empty(T, Hkv, D, dtype=torch.bfloat16, device=q.device) if want_k else None
+        ks = self.k_scale_cache if quant else None
+        vs = self.v_scale_cache if quant else None
+        num_blocks, block_size = kc.shape[0], kc.shape[1]
+        lib = _lib.load()
+        _lib.check(
+            lib.nvs_qk_norm_rope_store(
+                q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), k.stride(0), k.stride(1),
+                v.data_ptr(), v.stride(0), v.stride(1), pos.data_ptr(), T,
+                qw.data_ptr(), kw.data_ptr(), float(eps), table.data_ptr(), table.shape[0],
+                slots.data_ptr(), kc.data_ptr(), vc.data_ptr(), _lib.nvs_dtype(kc.dtype), _lib.ptr(ks),
+                _lib.ptr(vs), num_blocks, block_size, Hq, Hkv, D,
+                q_out.data_ptr(), q_out.stride(0), q_out.stride(1),
+                _lib.ptr(k_out), k_out.stride(0) if want_k else 0, k_out.stride(1) if want_k else 0,
+                _lib.stream_of(q),
+            ),
+            "qk_norm_rope_store",
+        )
+        return q_out, k_out
+
+    def forward_fused(self, q, k, v, positions, q_norm_weight, k_norm_weight, eps, cos_sin_cache, context):
+        """forward() for q and k before their norms and rotary embedding: the
+        fused pre-attention step (which writes the cache) and then the same
+        attention call forward_unified makes."""
+        local = context.block_tables is None
+        q_rot, k_rot = self.qk_norm_rope_store(q, k, v, positions, q_norm_weight, k_norm_weight, eps,
+                                               cos_sin_cache, context.slot_mapping, want_k=local)
+        if self.forward_backend == "torch":
+            return self.prefill_torch(q_rot, k_rot, v, context)
+        if self.forward_backend in ("flashattn", "hip"):
+            return self.prefill_flashattn(q_rot, k_rot, v, context)
+        raise NotImplementedError(f"unknown backend: {self.forward_backend}")
+
     def decode_flashattn(self, q, context):
         """Decode-only entry (attention.py:552-584): q [B, Hq, D] against the
         cache through context.block_tables / context_lens."""
