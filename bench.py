@@ -14,7 +14,7 @@ decode tokens/s (256 sequences, ctx U[1024, 4096], fp8 / int8 / bf16, seed
 4), the dominant kernel's roofline fraction (HIP events on the launch
 stream) and the CPU eager restatement timed on the host cores.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only decode|prefill|quant|mixed|prep]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only decode|prefill|quant|mixed|prep|context]
 """
 from __future__ import annotations
 
@@ -229,6 +229,92 @@ def bench_prep(steps, warmup):
     return out
 
 
+def context_kernel_us(seqs, steps, warmup):
+    """nvs_build_context alone (with the padded block table), launched back
+    to back on resident inputs."""
+    from nanovllm_self_amd import _lib
+
+    B, T = len(seqs), sum(s.num_new_tokens for s in seqs)
+    W = max(len(s.block_table) for s in seqs)
+    counts = torch.tensor([s.num_cached_tokens for s in seqs] + [s.num_new_tokens for s in seqs],
+                          dtype=torch.int32, device="cuda")
+    lens = [len(s.block_table) for s in seqs]
+    offsets = torch.tensor([sum(lens[:i]) for i in range(B + 1)], dtype=torch.int32, device="cuda")
+    ids = torch.tensor([x for s in seqs for x in s.block_table], dtype=torch.int32, device="cuda")
+    out = torch.empty(3 * B + 2 + T + B * W, dtype=torch.int32, device="cuda")
+    pos = torch.empty(T, dtype=torch.int64, device="cuda")
+    lib, st = _lib.load(), _lib.stream_of(out)
+    p = out.data_ptr()
+
+    def launch():
+        _lib.check(lib.nvs_build_context(counts.data_ptr(), counts.data_ptr() + 4 * B, B, offsets.data_ptr(),
+                                         ids.data_ptr(), ids.numel(), 256, T, p, p + 4 * (B + 1), p + 8 * (B + 1),
+                                         p + 4 * (3 * B + 2), pos.data_ptr(), p + 4 * (3 * B + 2 + T), W, st),
+                   "build_context")
+
+    _, ms = timed_steps(launch, steps, warmup)
+    return ms * 1e3
+
+
+def bench_context(steps, warmup):
+    """Step metadata for the measured batches: the device builder
+    (build_context_on_device: host packing + one pinned copy + one launch)
+    against the vectorised host builder (build_context), each timed to a
+    synchronised device Context; the CPU baseline is the reference's
+    per-token loop restated in Python plus the device tensors it makes from
+    the lists."""
+    from nanovllm_self_amd import workloads as W
+    from nanovllm_self_amd.kv_cache import build_context, build_context_on_device
+    from oracle import context_oracle as CO
+
+    dev = torch.device("cuda")
+    out = {"workload": "sequence lists of decode_8b, prefill_8b, decode_quant, mixed_32b (block 256)"}
+    for name, seqs in W.step_batches().items():
+        T = sum(s.num_new_tokens for s in seqs)
+
+        def host():
+            build_context(seqs, 256, dev)
+            torch.cuda.synchronize()
+
+        def device():
+            build_context_on_device(seqs, 256, dev)
+            torch.cuda.synchronize()
+
+        res = {"seqs": len(seqs), "tokens": T}
+        for label, fn in (("device", device), ("host", host)):
+            for _ in range(warmup):
+                fn()
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                fn()
+            res[f"{label}_us"] = (time.perf_counter() - t0) * 1e6 / steps
+        res["kernel_us"] = context_kernel_us(seqs, steps, warmup)
+        # CPU baseline: the reference's loop (restated) plus the device tensors
+        # it creates from the lists (model_runner.py:519-531, 334-344).
+        tup = [(s.block_table, s.num_cached_tokens, s.num_new_tokens, s.need_logits) for s in seqs]
+
+        def reference():
+            r = CO.prepare_model_input(tup, 256)
+            for f in ("cu_seqlens_q", "cu_seqlens_k", "slot_mapping", "context_lens", "seq_need_compute_logits"):
+                torch.tensor(r[f], dtype=torch.int32, device=dev)
+            torch.tensor(r["positions"], dtype=torch.int64, device=dev)
+            if r["block_tables"] is not None:
+                torch.tensor(r["block_tables"], dtype=torch.int32, pin_memory=True).to(dev)
+            torch.cuda.synchronize()
+
+        reference()
+        t0 = time.perf_counter()
+        reps = 0
+        while reps < 3 or time.perf_counter() - t0 < 0.5:
+            reference()
+            reps += 1
+        res["cpu_baseline_reference_us"] = (time.perf_counter() - t0) * 1e6 / reps
+        out[name] = res
+        log(f"context {name}: device {res['device_us']:.0f} us (kernel {res['kernel_us']:.1f}), host numpy "
+            f"{res['host_us']:.0f} us, reference loop + copies {res['cpu_baseline_reference_us']:.0f} us ({T} tokens)")
+    return out
+
+
 def bench_mixed(steps, warmup):
     from nanovllm_self_amd import workloads as W
 
@@ -326,7 +412,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", choices=["decode", "prefill", "quant", "mixed", "prep"], default=None)
+    ap.add_argument("--only", choices=["decode", "prefill", "quant", "mixed", "prep", "context"], default=None)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--calib-copy", action="store_true",
                     help="only run a 1 GiB device copy (for scaling PMC byte counters)")
@@ -358,6 +444,9 @@ def main():
         return
     if args.only == "prep":
         print(json.dumps(bench_prep(steps, warmup)))
+        return
+    if args.only == "context":
+        print(json.dumps(bench_context(steps, warmup)))
         return
 
     wl, dec = bench_decode(steps, warmup)
@@ -402,6 +491,7 @@ def main():
         line["decode_quant"] = bench_quant(steps, warmup)
         line["mixed_32b"] = bench_mixed(max(5, steps // 4), 2)
         line["qk_prep"] = bench_prep(steps, warmup)
+        line["step_context"] = bench_context(steps, warmup)
     print(json.dumps(line))
 
 

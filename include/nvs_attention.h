@@ -248,6 +248,40 @@ int nvs_varlen_attention(const void* q, int64_t q_tok_stride,
                          void* workspace, int64_t workspace_bytes,
                          void* stream);
 
+/*
+ * Step metadata built on the device.  Replaces the per-token loops of
+ * ModelRunner.prepare_model_input (reference model_runner.py:461-532) that
+ * form cu_seqlens_q/k, context_lens, positions and slot_mapping, and the
+ * padding of prepare_block_tables (model_runner.py:334-344).
+ *   num_cached_tokens, num_new_tokens  [num_seqs] int32: the Sequence fields
+ *                 the runner reads; num_seqs <= 4096.
+ *   block_ids     the sequences' block lists concatenated, int32
+ *                 [num_block_ids]; sequence b's list is block_ids[
+ *                 block_offsets[b] .. block_offsets[b+1]-1] (block_offsets
+ *                 int32 [num_seqs + 1]; offsets outside [0, num_block_ids]
+ *                 count as 0, a decreasing pair as an empty list).
+ *   num_tokens    the sum of num_new_tokens (the host knows it; it sizes
+ *                 slot_mapping and positions).
+ * Writes cu_seqlens_q / cu_seqlens_k [num_seqs + 1] (running sums of
+ * num_new and of num_cached + num_new), context_lens [num_seqs]
+ * (num_cached + num_new), and for query token t of sequence b at position
+ * p = num_cached[b] + (t - cu_seqlens_q[b]): positions[t] = p (int64; may
+ * be NULL) and slot_mapping[t] = list_b[p / block_size] * block_size +
+ * p % block_size.  A position past the end of its list or on a -1 entry gets
+ * slot -1 (the store skips it), as do tokens past the sum of num_new_tokens.
+ * block_tables (may be NULL) [num_seqs, block_table_width] receives each
+ * list padded (or cut) to the width with -1.  Slots and running sums are
+ * int32, as in the reference.
+ */
+int nvs_build_context(const int32_t* num_cached_tokens, const int32_t* num_new_tokens,
+                      int num_seqs, const int32_t* block_offsets,
+                      const int32_t* block_ids, int64_t num_block_ids,
+                      int block_size, int64_t num_tokens,
+                      int32_t* cu_seqlens_q, int32_t* cu_seqlens_k,
+                      int32_t* context_lens, int32_t* slot_mapping,
+                      int64_t* positions, int32_t* block_tables,
+                      int block_table_width, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -84,6 +84,15 @@ SIGNATURES = {
             _P, _L, _P,  # workspace, bytes, stream
         ],
     ),
+    "nvs_build_context": (
+        _I,
+        [
+            _P, _P, _I,  # num_cached, num_new, num_seqs
+            _P, _P, _L, _I, _L,  # block_offsets, block_ids, num_block_ids, block_size, num_tokens
+            _P, _P, _P, _P, _P,  # cu_q, cu_k, context_lens, slot_mapping, positions
+            _P, _I, _P,  # block_tables, width, stream
+        ],
+    ),
 }
 
 _lock = threading.Lock()

@@ -18,15 +18,20 @@ These are the producer side of the attention boundary in the reference:
 - prepare_block_tables mirrors model_runner.py:334-344 (rows padded with -1).
 - build_context mirrors prepare_model_input (model_runner.py:461-532) with the
   per-token slot loop vectorised.
+- build_context_on_device forms the same Context (plus the step's positions)
+  with one HIP launch (nvs_build_context): the host handles only per-sequence
+  counts and the padded block table, sent in one pinned copy.
 """
 from __future__ import annotations
 
 from dataclasses import dataclass
+from itertools import chain
 from typing import Iterable, Sequence
 
 import numpy as np
 import torch
 
+from . import _lib
 from .utils.context import Context, get_context
 
 KV_QUANT_MODES = ("none", "int8_mock", "fp8_e4m3")
@@ -180,3 +185,78 @@ def build_context(seqs: Sequence[SeqSlice], block_size: int, device) -> Context:
         block_tables=block_tables,
         seq_need_compute_logits=i32(need),
     )
+
+
+def build_context_on_device(seqs: Sequence[SeqSlice], block_size: int, device) -> tuple[Context, torch.Tensor]:
+    """prepare_model_input's step metadata (model_runner.py:461-532) formed on
+    the device; returns (context, positions int64 [T]).
+
+    The host touches each sequence once and each block id once: it packs
+    num_cached, num_new, the block-list offsets, the need-logits indices and
+    the concatenated block lists into one pinned int32 buffer and copies it
+    once; nvs_build_context expands them into cu_seqlens_q/k, context_lens,
+    slot_mapping, positions and the -1-padded block_tables.  The Context
+    equals build_context's, including block_tables None when no sequence has
+    cached tokens (:516-518).  A block list too short for a sequence's
+    positions raises IndexError, as the reference's seq.block_table[block_idx]
+    does (:505).
+    """
+    dev = torch.device(device)
+    if dev.type != "cuda":
+        raise RuntimeError("build_context_on_device needs a GPU device")
+    B = len(seqs)
+    meta = np.fromiter(
+        chain.from_iterable((s.num_cached_tokens, s.num_new_tokens, len(s.block_table), s.need_logits) for s in seqs),
+        dtype=np.int64, count=4 * B).reshape(B, 4)
+    cached, new, nblk = meta[:, 0], meta[:, 1], meta[:, 2]
+    lens = cached + new
+    if np.any(cached < 0) or np.any(new < 0):
+        raise ValueError("token counts must be non-negative")
+    short = (new > 0) & ((lens + block_size - 1) // block_size > nblk)
+    if np.any(short):
+        i = int(np.argmax(short))
+        raise IndexError(f"sequence {i}: block_table holds {int(nblk[i])} blocks, positions reach {int(lens[i]) - 1}")
+    n_ids = int(nblk.sum())
+    if int(lens.sum()) >= 2**31 or n_ids >= 2**31:
+        raise ValueError("step too large for int32 metadata")
+    T = int(new.sum())
+    need = np.flatnonzero(meta[:, 3])
+    n_need = len(need)
+    # Pinned staging: [cached B | new B | offsets B+1 | need | block ids]
+    o_off, o_need, o_ids = 2 * B, 3 * B + 1, 3 * B + 1 + n_need
+    staging = torch.empty(o_ids + n_ids, dtype=torch.int32, pin_memory=True)
+    host = staging.numpy()
+    host[:B] = cached
+    host[B:o_off] = new
+    host[o_off] = 0
+    np.cumsum(nblk, out=host[o_off + 1:o_need])
+    host[o_need:o_ids] = need
+    host[o_ids:] = np.fromiter(chain.from_iterable(s.block_table for s in seqs), dtype=np.int32, count=n_ids)
+    inputs = staging.to(dev, non_blocking=True)
+    W = max(int(nblk.max(initial=0)), 1)
+    with_table = int(cached.sum()) > 0
+    out = torch.empty(3 * B + 2 + T + (B * W if with_table else 0), dtype=torch.int32, device=dev)
+    positions = torch.empty(T, dtype=torch.int64, device=dev)
+    cu_q, cu_k = out[: B + 1], out[B + 1: 2 * B + 2]
+    ctx_lens, slots = out[2 * B + 2: 3 * B + 2], out[3 * B + 2: 3 * B + 2 + T]
+    table = out[3 * B + 2 + T:].view(B, W) if with_table else None
+    ip = inputs.data_ptr()
+    _lib.check(
+        _lib.load().nvs_build_context(
+            ip, ip + 4 * B, B, ip + 4 * o_off, ip + 4 * o_ids, n_ids, block_size, T,
+            cu_q.data_ptr(), cu_k.data_ptr(), ctx_lens.data_ptr(), slots.data_ptr(), positions.data_ptr(),
+            _lib.ptr(table), W if with_table else 0, _lib.stream_of(out),
+        ),
+        "build_context",
+    )
+    ctx = get_context(
+        cu_seqlens_q=cu_q,
+        cu_seqlens_k=cu_k,
+        max_seqlen_q=int(new.max(initial=0)),
+        max_seqlen_k=int(lens.max(initial=0)),
+        slot_mapping=slots,
+        context_lens=ctx_lens,
+        block_tables=table,
+        seq_need_compute_logits=inputs[o_need:o_ids],
+    )
+    return ctx, positions

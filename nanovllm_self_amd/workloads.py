@@ -164,12 +164,16 @@ def _tables(g, lens_total, bs, NB):
     return out
 
 
+def _decode_seqs(g, B, lo, hi, NB, bs):
+    ctx = torch.randint(lo, hi + 1, (B,), generator=g).tolist()
+    tables = _tables(g, ctx, bs, NB)
+    return [SeqSlice(tables[i], ctx[i] - 1, 1) for i in range(B)]
+
+
 def decode_workload(name, B, lo, hi, Hq, Hkv, NB, kv="bf16", seed=0, k_scale=1.0, outliers=False,
                     device="cuda", D=128, bs=256) -> Workload:
     g = _gen(seed)
-    ctx = torch.randint(lo, hi + 1, (B,), generator=g).tolist()
-    tables = _tables(g, ctx, bs, NB)
-    seqs = [SeqSlice(tables[i], ctx[i] - 1, 1) for i in range(B)]
+    seqs = _decode_seqs(g, B, lo, hi, NB, bs)
     return _assemble(name, seqs, Hq, Hkv, D, bs, NB, kv, device, g, k_scale, outliers, seed)
 
 
@@ -187,19 +191,20 @@ def decode_quant(device="cuda", kv="fp8", B=256) -> Workload:
                            device=device)
 
 
-def prefill_8b(device="cuda", kv="bf16", B=16, NB=512) -> Workload:
-    g = _gen(2)
-    bs = 256
+def _prefill_8b_seqs(g, B, NB, bs=256):
     prefix = [bs * int(x) for x in torch.randint(0, 9, (B,), generator=g).tolist()]
     new = torch.randint(512, 4097, (B,), generator=g).tolist()
     tables = _tables(g, [p + n for p, n in zip(prefix, new)], bs, NB)
-    seqs = [SeqSlice(tables[i], prefix[i], new[i]) for i in range(B)]
-    return _assemble("prefill_8b", seqs, 32, 8, 128, bs, NB, kv, device, g, seed=2)
+    return [SeqSlice(tables[i], prefix[i], new[i]) for i in range(B)]
 
 
-def mixed_32b(device="cuda", kv="bf16", n_decode=128, n_chunks=4, chunk=2048) -> Workload:
-    g = _gen(4)
-    bs, NB = 256, 16384
+def prefill_8b(device="cuda", kv="bf16", B=16, NB=512) -> Workload:
+    g = _gen(2)
+    seqs = _prefill_8b_seqs(g, B, NB)
+    return _assemble("prefill_8b", seqs, 32, 8, 128, 256, NB, kv, device, g, seed=2)
+
+
+def _mixed_32b_seqs(g, n_decode, n_chunks, chunk, bs=256, NB=16384):
     lo, hi = math.log(256), math.log(32768)
     u = torch.rand((n_decode,), generator=g, dtype=torch.float64)
     dec_ctx = [int(round(math.exp(lo + (hi - lo) * float(x)))) for x in u]
@@ -208,8 +213,25 @@ def mixed_32b(device="cuda", kv="bf16", n_decode=128, n_chunks=4, chunk=2048) ->
     totals = dec_ctx + [p + chunk for p in prefix]
     tables = _tables(g, totals, bs, NB)
     seqs = [SeqSlice(tables[i], dec_ctx[i] - 1, 1) for i in range(n_decode)]
-    seqs += [SeqSlice(tables[n_decode + j], prefix[j], chunk) for j in range(n_chunks)]
-    return _assemble("mixed_32b", seqs, 64, 8, 128, bs, NB, kv, device, g, seed=4)
+    return seqs + [SeqSlice(tables[n_decode + j], prefix[j], chunk) for j in range(n_chunks)]
+
+
+def mixed_32b(device="cuda", kv="bf16", n_decode=128, n_chunks=4, chunk=2048) -> Workload:
+    g = _gen(4)
+    seqs = _mixed_32b_seqs(g, n_decode, n_chunks, chunk)
+    return _assemble("mixed_32b", seqs, 64, 8, 128, 256, 16384, kv, device, g, seed=4)
+
+
+def step_batches() -> dict:
+    """The sequence lists (block size 256) of decode_8b, prefill_8b,
+    decode_quant and mixed_32b, drawn as their builders draw them, without
+    building any tensor."""
+    return {
+        "decode_8b": _decode_seqs(_gen(1), 64, 2048, 8192, 4096, 256),
+        "prefill_8b": _prefill_8b_seqs(_gen(2), 16, 512),
+        "decode_quant": _decode_seqs(_gen(3), 256, 1024, 4096, 4096, 256),
+        "mixed_32b": _mixed_32b_seqs(_gen(4), 128, 4, 2048),
+    }
 
 
 BUILDERS = {
