@@ -14,7 +14,7 @@ decode tokens/s (256 sequences, ctx U[1024, 4096], fp8 / int8 / bf16, seed
 4), the dominant kernel's roofline fraction (HIP events on the launch
 stream) and the CPU eager restatement timed on the host cores.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only decode|prefill|quant|mixed|prep|context]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only decode|prefill|quant|mixed|prep|context|handoff]
 """
 from __future__ import annotations
 
@@ -315,6 +315,54 @@ def bench_context(steps, warmup):
     return out
 
 
+def bench_handoff(steps, warmup):
+    """KV handoff copies at the Qwen3-8B cache shape (36 layers, 8 kv heads,
+    D 128, block 256): export of one 4096-token sequence's 16 blocks into a
+    snapshot and import of the snapshot into other blocks, against the
+    reference's torch expressions on the same GPU (kv_cache[:, :, ids]
+    .contiguous(); a copy_ per block)."""
+    from nanovllm_self_amd.kv_cache import (KVCacheConfig, allocate_kv_cache, export_kv_blocks,
+                                            import_kv_blocks)
+
+    L, Hkv, D, bs, NB, n = 36, 8, 128, 256, 128, 16
+    out = {"workload": f"Qwen3-8B cache ({L} layers, {Hkv} kv heads, D{D}, block {bs}, {NB}-block pool); "
+                       f"{n} blocks (one 4096-token sequence) exported and imported"}
+    for kv, dt, mode in (("bf16", torch.bfloat16, "none"), ("fp8", torch.float8_e4m3fn, "fp8_e4m3")):
+        cfg = KVCacheConfig(dtype=torch.bfloat16, kv_cache_dtype=dt, attention_compute_dtype=torch.bfloat16,
+                            kv_cache_quant_mode=mode, block_size=bs, num_blocks=NB)
+        kvc, sc = allocate_kv_cache(L, Hkv, D, cfg, "cuda")
+        g = torch.Generator().manual_seed(6)
+        perm = torch.randperm(NB, generator=g).tolist()
+        src_ids, dst_ids = perm[:n], perm[n:2 * n]
+        blocks, scales = export_kv_blocks(kvc, sc, src_ids)
+        moved = 2 * (blocks.numel() * blocks.element_size() + (scales.numel() * 4 if scales is not None else 0))
+
+        def ref_export():
+            kvc[:, :, src_ids].contiguous()
+            if sc is not None:
+                sc[:, :, src_ids].contiguous()
+
+        def ref_import():
+            for i, b in enumerate(dst_ids):
+                kvc[:, :, b].copy_(blocks[:, :, i])
+                if sc is not None:
+                    sc[:, :, b].copy_(scales[:, :, i])
+
+        res = {"bytes_moved": moved}
+        for label, fn in (("export", lambda: export_kv_blocks(kvc, sc, src_ids)),
+                          ("import", lambda: import_kv_blocks(kvc, sc, blocks, scales, dst_ids)),
+                          ("ref_export", ref_export), ("ref_import", ref_import)):
+            _, ms = timed_steps(fn, steps, warmup)
+            res[f"{label}_us"] = ms * 1e3
+            res[f"{label}_gbs"] = moved / ms / 1e6
+        out[kv] = res
+        log(f"handoff {kv}: export {res['export_us']:.0f} us ({res['export_gbs']:.0f} GB/s), import "
+            f"{res['import_us']:.0f} us; torch: {res['ref_export_us']:.0f} / {res['ref_import_us']:.0f} us")
+        del kvc, sc, blocks, scales
+        torch.cuda.empty_cache()
+    return out
+
+
 def bench_mixed(steps, warmup):
     from nanovllm_self_amd import workloads as W
 
@@ -412,7 +460,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", choices=["decode", "prefill", "quant", "mixed", "prep", "context"], default=None)
+    ap.add_argument("--only", choices=["decode", "prefill", "quant", "mixed", "prep", "context", "handoff"], default=None)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--calib-copy", action="store_true",
                     help="only run a 1 GiB device copy (for scaling PMC byte counters)")
@@ -447,6 +495,9 @@ def main():
         return
     if args.only == "context":
         print(json.dumps(bench_context(steps, warmup)))
+        return
+    if args.only == "handoff":
+        print(json.dumps(bench_handoff(steps, warmup)))
         return
 
     wl, dec = bench_decode(steps, warmup)
@@ -492,6 +543,7 @@ def main():
         line["mixed_32b"] = bench_mixed(max(5, steps // 4), 2)
         line["qk_prep"] = bench_prep(steps, warmup)
         line["step_context"] = bench_context(steps, warmup)
+        line["kv_handoff"] = bench_handoff(steps, warmup)
     print(json.dumps(line))
 
 

@@ -282,6 +282,29 @@ int nvs_build_context(const int32_t* num_cached_tokens, const int32_t* num_new_t
                       int64_t* positions, int32_t* block_tables,
                       int block_table_width, void* stream);
 
+/*
+ * Whole-block copies between a paged cache and a packed block snapshot, one
+ * launch per tensor.  Replaces the KV handoff copies of the reference's PD
+ * connector: the export kv_cache[:, :, src_block_ids].contiguous() (and the
+ * same of kv_scale_cache) in _export_kv_snapshot
+ * (pd_self/kv_connector.py:94-110), and the per-block loop
+ * kv_cache[:, :, block_id].copy_(blocks[:, :, i]) of load_kv_item
+ * (kv_connector.py:282-311).
+ *   src, dst      [num_planes, src/dst_num_blocks, block_bytes] byte arrays
+ *                 (num_planes = 2 x layers; block_bytes = block_size x
+ *                 kv_heads x head_dim x element size for the codes,
+ *                 block_size x kv_heads x 4 for the fp32 scales), 16-byte
+ *                 aligned, block_bytes a multiple of 16.
+ *   copy i moves block src_block_ids[i] (i when NULL) of every plane to block
+ *   dst_block_ids[i] (i when NULL) of the same plane.  Ids outside
+ *   [0, num_blocks) skip the copy.  Destinations must be distinct and the
+ *   source and destination regions disjoint (copies run in no fixed order).
+ */
+int nvs_copy_blocks(const void* src, int64_t src_num_blocks, const int32_t* src_block_ids,
+                    void* dst, int64_t dst_num_blocks, const int32_t* dst_block_ids,
+                    int64_t num_planes, int64_t block_bytes, int64_t num_copies,
+                    void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -93,6 +93,7 @@ SIGNATURES = {
             _P, _I, _P,  # block_tables, width, stream
         ],
     ),
+    "nvs_copy_blocks": (_I, [_P, _L, _P, _P, _L, _P, _L, _L, _L, _P]),
 }
 
 _lock = threading.Lock()

@@ -18,12 +18,16 @@ These are the producer side of the attention boundary in the reference:
 - prepare_block_tables mirrors model_runner.py:334-344 (rows padded with -1).
 - build_context mirrors prepare_model_input (model_runner.py:461-532) with the
   per-token slot loop vectorised.
+- export_kv_blocks / import_kv_blocks are the KV handoff copies of the PD
+  connector (pd_self/kv_connector.py:65-135, 264-311): whole cache blocks,
+  codes and fp32 scales alike, moved by one launch per tensor.
 - build_context_on_device forms the same Context (plus the step's positions)
   with one HIP launch (nvs_build_context): the host handles only per-sequence
   counts and the padded block table, sent in one pinned copy.
 """
 from __future__ import annotations
 
+import math
 from dataclasses import dataclass
 from itertools import chain
 from typing import Iterable, Sequence
@@ -260,3 +264,74 @@ def build_context_on_device(seqs: Sequence[SeqSlice], block_size: int, device) -
         seq_need_compute_logits=inputs[o_need:o_ids],
     )
     return ctx, positions
+
+
+def _device_ids(ids: Sequence[int], num_blocks: int, device) -> torch.Tensor:
+    """Block ids as an int32 device tensor; an id outside the cache raises
+    IndexError, as indexing the reference's cache tensor does."""
+    host = np.asarray(list(ids), dtype=np.int64)
+    if host.size and (host.min() < 0 or host.max() >= num_blocks):
+        raise IndexError(f"block id out of range for a cache of {num_blocks} blocks")
+    return torch.from_numpy(host.astype(np.int32)).pin_memory().to(device, non_blocking=True)
+
+
+def _copy_blocks(src: torch.Tensor, src_ids, dst: torch.Tensor, dst_ids, n: int) -> None:
+    """Copy n blocks of every plane between two [2, L, num_blocks, ...]
+    tensors; src_ids / dst_ids are int32 device tensors or None (identity)."""
+    if not (src.is_contiguous() and dst.is_contiguous()):
+        raise RuntimeError("block copies need contiguous caches and snapshots")
+    if src.dtype != dst.dtype or src.shape[:2] != dst.shape[:2] or src.shape[3:] != dst.shape[3:]:
+        raise RuntimeError(f"block shapes differ: {tuple(src.shape)} {src.dtype} vs {tuple(dst.shape)} {dst.dtype}")
+    planes = src.shape[0] * src.shape[1]
+    block_bytes = math.prod(src.shape[3:]) * src.element_size()
+    _lib.check(
+        _lib.load().nvs_copy_blocks(
+            src.data_ptr(), src.shape[2], _lib.ptr(src_ids), dst.data_ptr(), dst.shape[2], _lib.ptr(dst_ids),
+            planes, block_bytes, n, _lib.stream_of(dst),
+        ),
+        "copy_blocks",
+    )
+
+
+def export_kv_blocks(kv_cache: torch.Tensor, kv_scale_cache: torch.Tensor | None, block_ids: Sequence[int]):
+    """kv_cache[:, :, block_ids].contiguous() and the same of the scale cache
+    (None when there is none), formed on the device: the snapshot of
+    KVConnector._export_kv_snapshot's device-direct path
+    (kv_connector.py:94-110).  Quantised caches export their codes and fp32
+    scales as they are stored."""
+    dev = kv_cache.device
+    n = len(block_ids)
+    ids = _device_ids(block_ids, kv_cache.shape[2], dev)
+    kv_blocks = torch.empty((*kv_cache.shape[:2], n, *kv_cache.shape[3:]), dtype=kv_cache.dtype, device=dev)
+    _copy_blocks(kv_cache, ids, kv_blocks, None, n)
+    scale_blocks = None
+    if kv_scale_cache is not None:
+        scale_blocks = torch.empty((*kv_scale_cache.shape[:2], n, *kv_scale_cache.shape[3:]),
+                                   dtype=kv_scale_cache.dtype, device=dev)
+        _copy_blocks(kv_scale_cache, ids, scale_blocks, None, n)
+    return kv_blocks, scale_blocks
+
+
+def import_kv_blocks(kv_cache: torch.Tensor, kv_scale_cache: torch.Tensor | None, kv_blocks: torch.Tensor,
+                     scale_blocks: torch.Tensor | None, dst_block_ids: Sequence[int]) -> None:
+    """kv_cache[:, :, dst_block_ids[i]] = kv_blocks[:, :, i] for each i, and
+    the same for the scales: KVConnector.load_kv_item (kv_connector.py:264-311)
+    in one launch per tensor.  Host snapshots are copied to the device first
+    (non-blocking, as the reference does).  When an id repeats, the last copy
+    wins, as in the reference's sequential loop."""
+    if kv_blocks is None or not len(dst_block_ids):
+        return
+    if scale_blocks is not None and kv_scale_cache is None:
+        raise RuntimeError("received scale_blocks but decode runner has no kv_scale_cache")
+    dev = kv_cache.device
+    ids = list(dst_block_ids)
+    if len(ids) > kv_blocks.shape[2]:
+        raise IndexError(f"{len(ids)} destination blocks for a snapshot of {kv_blocks.shape[2]}")
+    last = {b: i for i, b in enumerate(ids)}
+    src_idx = sorted(last.values())
+    dst = _device_ids([ids[i] for i in src_idx], kv_cache.shape[2], dev)
+    src = None if len(src_idx) == len(ids) else _device_ids(src_idx, kv_blocks.shape[2], dev)
+    kv_dev = kv_blocks.to(dev, non_blocking=True)
+    _copy_blocks(kv_dev, src, kv_cache, dst, len(src_idx))
+    if scale_blocks is not None:
+        _copy_blocks(scale_blocks.to(dev, non_blocking=True), src, kv_scale_cache, dst, len(src_idx))
