@@ -26,7 +26,9 @@
 // o[128]) per query head in each wave, merged by decode_merge_kernel with a
 // log-sum-exp (a second launch: the kernel boundary makes the partials
 // visible across XCDs without device-scope fences, which on a multi-XCD part
-// write back the L2).
+// write back the L2).  The group where a split row starts leaves a record
+// (output row, last group, slot) for the merge, so the merge needs no scan
+// of its own.
 #include <algorithm>
 
 #include "nvs_common.h"
@@ -47,6 +49,7 @@ struct DecodeArgs {
   float scale_log2;
   float* ws_o;   // [max_waves, 2 slots, g, 128]
   float* ws_ml;  // [max_waves, 2 slots, g, 2]
+  int32_t* ws_rec;  // [4 + 4 waves]: (T, Kw), then per wave the split row it merges
   const int32_t* cu_q;
   const int32_t* cu_k;
   int B;
@@ -424,13 +427,39 @@ __device__ __forceinline__ int wave_incl_scan(int v) {
   return v;
 }
 
+// Zeroes the output of the round's decode rows that see no key (row b by
+// wave b % gridDim.x): no tile covers them, so no wave writes them otherwise.
+__device__ __forceinline__ void zero_keyless_rows(const DecodeArgs& a, const ScanRound& rd) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int i = 0; i < kScanRows; ++i) {
+    const int b = rd.c0 + kScanRows * lane + i;
+    const bool dec = rd.q[i + 1] - rd.q[i] == 1 && rd.q[i] >= 0 && (int64_t)rd.q[i + 1] <= a.T;
+    uint64_t z = __ballot(b < a.B && dec && rd.k[i + 1] - rd.k[i] <= 0 && b % (int)gridDim.x == (int)blockIdx.x);
+    while (z) {
+      const int li = __builtin_ctzll(z);
+      z &= z - 1;
+      const int q0 = __builtin_amdgcn_readlane(rd.q[i], li);
+      for (int x = lane; x < a.Hq * (kHeadDim / 8); x += 64) {
+        const int hq = x / (kHeadDim / 8), d = 8 * (x % (kHeadDim / 8));
+        *reinterpret_cast<u32x4*>(a.out + (int64_t)q0 * a.out_ts + (int64_t)hq * a.out_hs + d) = u32x4{0, 0, 0, 0};
+      }
+    }
+  }
+}
+
 // Total decode tiles of the batch; r0 receives the first scan round, which
-// locate_tile reuses.
+// locate_tile reuses.  Keyless decode rows are zeroed on the way.
 __device__ __forceinline__ int decode_tiles(const DecodeArgs& a, const int32_t* __restrict__ cu_q,
                                             const int32_t* __restrict__ cu_k, ScanRound& r0) {
   r0 = load_round(a, cu_q, cu_k, 0);
   int tot = wave_sum_i(lane_tiles(a, r0));
-  for (int c0 = kScanSpan; c0 < a.B; c0 += kScanSpan) tot += wave_sum_i(lane_tiles(a, load_round(a, cu_q, cu_k, c0)));
+  zero_keyless_rows(a, r0);
+  for (int c0 = kScanSpan; c0 < a.B; c0 += kScanSpan) {
+    const ScanRound rd = load_round(a, cu_q, cu_k, c0);
+    tot += wave_sum_i(lane_tiles(a, rd));
+    zero_keyless_rows(a, rd);
+  }
   return tot;
 }
 
@@ -623,7 +652,11 @@ void paged_decode_kernel(DecodeArgs a, const int32_t* __restrict__ bt, const int
   ScanRound r0;
   const int T = decode_tiles(a, cu_q, cu_k, r0);
   const int Kw = decode_groups(T, G);
-  if (k >= Kw) return;
+  if (w == 0 && lane < 2) a.ws_rec[lane] = lane == 0 ? T : Kw;
+  if (k >= Kw) {
+    if (lane == 0) a.ws_rec[4 + 4 * w + 3] = 0;
+    return;
+  }
   const int s0 = group_start(T, Kw, k);
   const int left = group_start(T, Kw, k + 1) - s0;  // >= 1 (Kw <= T)
 
@@ -680,6 +713,16 @@ void paged_decode_kernel(DecodeArgs a, const int32_t* __restrict__ bt, const int
       decode_tile_compute<KV, false>(cur, qop, o, m_run, l_run, kt, c.K, grp, a.scale_log2);
     __builtin_amdgcn_sched_barrier(0);
     if (c.t == c.n - 1 || i == left - 1) {  // the segment ends with tile i
+      if (i == left - 1 && lane < 4) {
+        // The wave's record: its last row (output row, tiles left after the
+        // group's range, partial slot), valid if the row continues past the
+        // range and starts inside it (this group merges it).
+        const int v = lane == 0   ? c.q0
+                      : lane == 1 ? c.n - 1 - c.t
+                      : lane == 2 ? slot
+                                  : (int)(c.t != c.n - 1 && seg_t0 == 0);
+        a.ws_rec[4 + 4 * w + lane] = v;
+      }
       float l = l_run + shfl_xor(l_run, 16);
       l += shfl_xor(l, 32);
       finish_segment(a, c, h, seg_t0 == 0 && c.t == c.n - 1, w, slot, o, m_run, l, col, grp);
@@ -708,53 +751,26 @@ void paged_decode_kernel(DecodeArgs a, const int32_t* __restrict__ bt, const int
   }
 }
 
-// Log-sum-exp merge of the rows split across groups (and the zeroing of
-// decode rows without a visible key).  Wave k Hkv + h owns kv head h of the
-// row that crosses the boundary after group k if that row starts inside
-// group k's range; its partials sit in wave k Hkv + h (slot 0 if the row is
-// the group's first segment, else slot 1) and in waves x Hkv + h for groups
-// x = k + 1 .. k_last (slot 0).  Lane l serves head 4 p + l / 16 of the
-// group (pass p) and head_dim elements 8 (l % 16) .. + 7; one pass over the
-// partials keeps a running max, sum and output, with the loads of four
-// partials in flight at a time.
-__global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a, int groups, const int32_t* __restrict__ cu_q,
-                                                         const int32_t* __restrict__ cu_k) {
+// Log-sum-exp merge of the rows split across groups.  Wave k Hkv + h owns kv
+// head h of the row recorded by decode wave k Hkv + h (the row that crosses
+// the boundary after group k and starts inside group k's range); its
+// partials sit in wave
+// k Hkv + h (the recorded slot) and in waves x Hkv + h for groups x = k + 1
+// .. k_last (slot 0).  Lane l serves head 4 p + l / 16 of the group (pass p)
+// and head_dim elements 8 (l % 16) .. + 7; one pass over the partials keeps
+// a running max, sum and output, with the loads of four partials in flight
+// at a time.
+__global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a) {
   const int k = blockIdx.x / a.Hkv, h = blockIdx.x - k * a.Hkv;
   const int lane = threadIdx.x;
-  // Tiles, and the zeroing of decode rows without a visible key (row b by
-  // merge wave b % gridDim.x).
-  const ScanRound r0 = load_round(a, cu_q, cu_k, 0);
-  int T = 0;
-  for (int c0 = 0; c0 < a.B; c0 += kScanSpan) {
-    const ScanRound rd = c0 == 0 ? r0 : load_round(a, cu_q, cu_k, c0);
-    T += wave_sum_i(lane_tiles(a, rd));
-#pragma unroll
-    for (int i = 0; i < kScanRows; ++i) {
-      const int b = rd.c0 + kScanRows * lane + i;
-      const bool dec = rd.q[i + 1] - rd.q[i] == 1 && rd.q[i] >= 0 && (int64_t)rd.q[i + 1] <= a.T;
-      uint64_t z = __ballot(b < a.B && dec && rd.k[i + 1] - rd.k[i] <= 0 && b % (int)gridDim.x == (int)blockIdx.x);
-      while (z) {
-        const int li = __builtin_ctzll(z);
-        z &= z - 1;
-        const int q0 = __builtin_amdgcn_readlane(rd.q[i], li);
-        for (int x = lane; x < a.Hq * (kHeadDim / 8); x += 64) {
-          const int hq = x / (kHeadDim / 8), d = 8 * (x % (kHeadDim / 8));
-          *reinterpret_cast<u32x4*>(a.out + (int64_t)q0 * a.out_ts + (int64_t)hq * a.out_hs + d) = u32x4{0, 0, 0, 0};
-        }
-      }
-    }
-  }
-  const int Kw = decode_groups(T, groups);
-  if (k + 1 >= Kw) return;
-  Cursor r;
-  int first;  // the first tile of the row at the boundary after group k
-  locate_tile(a, cu_q, cu_k, group_start(T, Kw, k + 1), r0, r, first);
-  if (r.t == 0) return;  // the boundary falls between rows
-  const int sk = group_start(T, Kw, k);
-  if (first < sk) return;  // started in an earlier group, which merges it
-  const int last = first + r.n - 1;
+  const int32_t* rec = a.ws_rec + 4 + 4 * blockIdx.x;
+  if (__builtin_amdgcn_readfirstlane(rec[3]) == 0) return;
+  const int T = __builtin_amdgcn_readfirstlane(a.ws_rec[0]);
+  const int Kw = __builtin_amdgcn_readfirstlane(a.ws_rec[1]);
+  const int q_row = __builtin_amdgcn_readfirstlane(rec[0]);
+  const int last = group_start(T, Kw, k + 1) - 1 + __builtin_amdgcn_readfirstlane(rec[1]);  // the row's last tile
   const int k_last = (int)(((int64_t)(last + 1) * Kw - 1) / T);
-  const int slot_k = first != sk ? 1 : 0;
+  const int slot_k = __builtin_amdgcn_readfirstlane(rec[2]);
   const int j = lane & 15;
   for (int c0 = 0; c0 < a.g; c0 += 4) {
     const int c = c0 + (lane >> 4);
@@ -792,13 +808,16 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a, int grou
       v[1] = pack_bf16x2(acc0[2] * inv, acc0[3] * inv);
       v[2] = pack_bf16x2(acc1[0] * inv, acc1[1] * inv);
       v[3] = pack_bf16x2(acc1[2] * inv, acc1[3] * inv);
-      *reinterpret_cast<u32x4*>(a.out + (int64_t)r.q0 * a.out_ts + (int64_t)(h * a.g + c) * a.out_hs + 8 * j) = v;
+      *reinterpret_cast<u32x4*>(a.out + (int64_t)q_row * a.out_ts + (int64_t)(h * a.g + c) * a.out_hs + 8 * j) = v;
     }
   }
 }
 
 int64_t decode_workspace_bytes(int max_waves, int group) {
-  return (int64_t)max_waves * 2 * group * (kHeadDim + 2) * (int64_t)sizeof(float);
+  // Partials, then a 4-int header and one 4-int record per wave (sized for
+  // the most waves any call launches, so the size only grows with group).
+  return (int64_t)max_waves * 2 * group * (kHeadDim + 2) * (int64_t)sizeof(float) +
+         ((int64_t)kDecodeMaxWaves + 1) * 4 * (int64_t)sizeof(int32_t);
 }
 
 int launch_decode(const AttnParams& P, int max_waves, int waves, void* partials, hipStream_t stream) {
@@ -812,6 +831,7 @@ int launch_decode(const AttnParams& P, int max_waves, int waves, void* partials,
   a.out = (uint16_t*)P.out; a.out_ts = P.out_ts; a.out_hs = P.out_hs;
   a.ws_o = (float*)partials;
   a.ws_ml = a.ws_o + (int64_t)max_waves * 2 * a.g * kHeadDim;
+  a.ws_rec = (int32_t*)(a.ws_ml + (int64_t)max_waves * 2 * a.g * 2);
   if (waves <= 0) return NVS_OK;
   dim3 grid(waves), block(64);
   switch (P.cache_dtype) {
@@ -831,11 +851,11 @@ int launch_decode(const AttnParams& P, int max_waves, int waves, void* partials,
   }
   int rc = check_launch("paged_decode");
   if (rc != NVS_OK) return rc;
-  // The merge also zeroes decode rows without a visible key, so it runs even
-  // when a single group cannot leave split rows.
+  // With one group no row is split (keyless rows were zeroed by the decode
+  // kernel's scan).
   const int groups = waves / P.Hkv;
-  hipLaunchKernelGGL(decode_merge_kernel, dim3(std::max(groups - 1, 1) * P.Hkv), dim3(64), 0, stream, a, groups,
-                     P.cu_q, P.cu_k);
+  if (groups <= 1) return NVS_OK;
+  hipLaunchKernelGGL(decode_merge_kernel, dim3((groups - 1) * P.Hkv), dim3(64), 0, stream, a);
   return check_launch("decode_merge");
 }
 
