@@ -15,11 +15,14 @@
 // Each product and sum is rounded on its own (no fused multiply-add), as the
 // eager torch ops compute them.
 //
-// Work: 16 lanes per (token, unit) row, units = Hq query heads, then Hkv key
-// heads, then Hkv value heads (four rows per wave); lane j holds elements
-// 8 j .. 8 j + 7 of its head (head_dim 128) as one 16-byte load, its rotary
-// partners (elements +-64) sit in lane j ^ 8, and the norm's sum is a
-// butterfly over the row's 16 lanes.
+// Work: one wave per token.  Its rows (units) are the Hq query heads, then
+// the Hkv key heads, then the Hkv value heads; the wave's four 16-lane groups
+// take rows g, g + 4, g + 8, ..., four passes at a time with every load of
+// the four issued before any is used.  Lane j holds elements 8 j .. 8 j + 7
+// of its head (head_dim 128) as one 16-byte load, its rotary partners
+// (elements +-64) sit in lane j ^ 8, and the norm's sum is a butterfly over
+// the row's 16 lanes.  The token's position, cos/sin and the two norm
+// weights are loaded once per wave.
 #include <algorithm>
 
 #include "nvs_common.h"
@@ -32,6 +35,8 @@ namespace {
 constexpr int kPrepD = 128;
 constexpr int kRowLanes = 16;  // lanes per head row, 8 elements each
 constexpr int kPrepThreads = 256;
+constexpr int kPrepTokens = kPrepThreads / 64;  // one wave per token
+constexpr int kPrepUnroll = 4;                  // passes whose loads are issued together
 
 struct PrepArgs {
   const uint16_t* q;
@@ -66,10 +71,6 @@ __device__ __forceinline__ float bf16r(float x) { return bf16_bits_to_f32(f32_to
 __device__ __forceinline__ float mul_rn(float a, float b) {
 #pragma clang fp contract(off)
   return a * b;
-}
-__device__ __forceinline__ float sub_rn(float a, float b) {
-#pragma clang fp contract(off)
-  return a - b;
 }
 __device__ __forceinline__ float add_rn(float a, float b) {
 #pragma clang fp contract(off)
@@ -123,68 +124,94 @@ __device__ __forceinline__ void cache_row(void* cache, float* scales, int64_t ro
 
 template <int DST>
 __global__ __launch_bounds__(kPrepThreads) void qk_prep_kernel(PrepArgs a) {
+  // The token is wave-uniform (through readfirstlane, so its pointers are
+  // scalar); a lane adds a 32-bit offset for its head row and elements.
+  const int64_t t = (int64_t)blockIdx.x * kPrepTokens + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (t >= a.T) return;  // whole waves exit together
   const int U = a.Hq + 2 * a.Hkv;
-  const int64_t rows = a.T * U;
-  const int64_t unit = ((int64_t)blockIdx.x * kPrepThreads + threadIdx.x) / kRowLanes;
-  if (unit >= rows) return;  // whole rows exit together
-  const int64_t t = unit / U;
-  const int u = (int)(unit - t * U);
-  const int j = threadIdx.x & (kRowLanes - 1);
+  const int g = (threadIdx.x >> 4) & 3, j = threadIdx.x & (kRowLanes - 1);
   const int64_t slot = a.slots[t];
   const bool ok = slot >= 0 && slot < a.total_slots;
+  const int64_t cslot = ok ? slot : 0;
 
-  if (u >= a.Hq + a.Hkv) {  // value head: cast / quantise into the cache
-    const int h = u - a.Hq - a.Hkv;
-    float x[8];
-    load8<NVS_DTYPE_BF16>(a.v + t * a.v_ts + (int64_t)h * a.v_hs + 8 * j, x);
-    cache_row<DST>(a.vc, a.vs, (ok ? slot : 0) * a.Hkv + h, x, ok);
-    return;
-  }
-  const bool is_q = u < a.Hq;
-  const int h = is_q ? u : u - a.Hq;
-  float x[8], w[8];
-  load8<NVS_DTYPE_BF16>(is_q ? a.q + t * a.q_ts + (int64_t)h * a.q_hs + 8 * j
-                             : a.k + t * a.k_ts + (int64_t)h * a.k_hs + 8 * j,
-                        x);
-  load8<NVS_DTYPE_BF16>((is_q ? a.qw : a.kw) + 8 * j, w);
-
-  // RMSNorm: mean of squares over the 128 elements (division by 128 is exact).
-  float ss = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) ss = add_rn(ss, mul_rn(x[i], x[i]));
-  ss = row_sum16(ss);
-  // __builtin_sqrtf is the correctly rounded square root (HIP's __fsqrt_rn
-  // is the raw v_sqrt_f32 here, off by an ulp at times).
-  const float rms = __builtin_sqrtf(add_rn(mul_rn(ss, 1.0f / kPrepD), a.eps));
-  float n[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) n[i] = bf16r(__fdiv_rn(mul_rn(w[i], x[i]), rms));
-
-  // Rotary pairs (e, e + 64): lanes j and j ^ 8 hold the two halves.
+  // Per token: rotary cos / sin of the lane's elements and the norm weights.
   int64_t p = a.pos[t];
   p = p < 0 ? 0 : (p >= a.max_pos ? a.max_pos - 1 : p);
   const float* cs = a.cs + p * kPrepD + 8 * (j & 7);
-  float c[8], s[8];
+  float c[8], s[8], qw[8], kw[8];
   *reinterpret_cast<f32x4*>(c) = *reinterpret_cast<const f32x4*>(cs);
   *reinterpret_cast<f32x4*>(c + 4) = *reinterpret_cast<const f32x4*>(cs + 4);
   *reinterpret_cast<f32x4*>(s) = *reinterpret_cast<const f32x4*>(cs + 64);
   *reinterpret_cast<f32x4*>(s + 4) = *reinterpret_cast<const f32x4*>(cs + 68);
+  load8<NVS_DTYPE_BF16>(a.qw + 8 * j, qw);
+  load8<NVS_DTYPE_BF16>(a.kw + 8 * j, kw);
   const bool first = j < 8;
-  float y[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const float other = row_xor<8>(n[i]);
-    // first half: y1 = x1 cos - x2 sin; second half: y2 = x2 cos + x1 sin
-    y[i] = first ? bf16r(sub_rn(mul_rn(n[i], c[i]), mul_rn(other, s[i])))
-                 : bf16r(add_rn(mul_rn(n[i], c[i]), mul_rn(other, s[i])));
-  }
+  const uint16_t* const q_tok = a.q + t * a.q_ts;
+  const uint16_t* const k_tok = a.k + t * a.k_ts;
+  const uint16_t* const v_tok = a.v + t * a.v_ts;
+  uint16_t* const qo_tok = a.qo + t * a.qo_ts;
+  uint16_t* const ko_tok = a.ko ? a.ko + t * a.ko_ts : nullptr;
 
-  if (is_q) {
-    store8_float<NVS_DTYPE_BF16>(a.qo + t * a.qo_ts + (int64_t)h * a.qo_hs + 8 * j, y);
-    return;
+  const int passes = (U + 3) / 4;
+  for (int i0 = 0; i0 < passes; i0 += kPrepUnroll) {
+    float x[kPrepUnroll][8];
+#pragma unroll
+    for (int k = 0; k < kPrepUnroll; ++k) {
+      const int u = g + 4 * (i0 + k);
+      if (u >= U) continue;
+      const uint16_t* src;
+      int off;
+      if (u < a.Hq) {
+        src = q_tok;
+        off = u * (int)a.q_hs;
+      } else if (u < a.Hq + a.Hkv) {
+        src = k_tok;
+        off = (u - a.Hq) * (int)a.k_hs;
+      } else {
+        src = v_tok;
+        off = (u - a.Hq - a.Hkv) * (int)a.v_hs;
+      }
+      load8<NVS_DTYPE_BF16>(src + (uint32_t)(off + 8 * j), x[k]);
+    }
+#pragma unroll
+    for (int k = 0; k < kPrepUnroll; ++k) {
+      const int u = g + 4 * (i0 + k);
+      if (u >= U) continue;
+      if (u >= a.Hq + a.Hkv) {  // value head: cast / quantise into the cache
+        cache_row<DST>(a.vc, a.vs, cslot * a.Hkv + (u - a.Hq - a.Hkv), x[k], ok);
+        continue;
+      }
+      const bool is_q = u < a.Hq;
+      const int h = is_q ? u : u - a.Hq;
+      // RMSNorm: mean of squares over the 128 elements (division by 128 is exact).
+      float ss = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ss = add_rn(ss, mul_rn(x[k][i], x[k][i]));
+      ss = row_sum16(ss);
+      // __builtin_sqrtf is the correctly rounded square root (HIP's __fsqrt_rn
+      // is the raw v_sqrt_f32 here, off by an ulp at times).
+      const float rms = __builtin_sqrtf(add_rn(mul_rn(ss, 1.0f / kPrepD), a.eps));
+      float n[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) n[i] = bf16r(__fdiv_rn(mul_rn(is_q ? qw[i] : kw[i], x[k][i]), rms));
+      // Rotary pairs (e, e + 64): lanes j and j ^ 8 hold the two halves.
+      // first half: y1 = x1 cos - x2 sin; second half: y2 = x2 cos + x1 sin.
+      // a - b and a + (-b) round identically, so both halves are one add of
+      // a product whose factor carries the sign.
+      float y[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float other = row_xor<8>(n[i]);
+        y[i] = bf16r(add_rn(mul_rn(n[i], c[i]), mul_rn(first ? -other : other, s[i])));
+      }
+      if (is_q) {
+        store8_float<NVS_DTYPE_BF16>(qo_tok + (uint32_t)(h * (int)a.qo_hs + 8 * j), y);
+        continue;
+      }
+      if (ko_tok) store8_float<NVS_DTYPE_BF16>(ko_tok + (uint32_t)(h * (int)a.ko_hs + 8 * j), y);
+      cache_row<DST>(a.kc, a.ks, cslot * a.Hkv + h, y, ok);
+    }
   }
-  if (a.ko) store8_float<NVS_DTYPE_BF16>(a.ko + t * a.ko_ts + (int64_t)h * a.ko_hs + 8 * j, y);
-  cache_row<DST>(a.kc, a.ks, (ok ? slot : 0) * a.Hkv + h, y, ok);
 }
 
 bool is_code_dtype(int dt) { return dt == NVS_DTYPE_INT8 || dt == NVS_DTYPE_FP8_E4M3; }
@@ -225,14 +252,15 @@ extern "C" int nvs_qk_norm_rope_store(const void* q, int64_t q_tok_stride, int64
               NVS_ERR_UNSUPPORTED, "%s: cache dtype %d", who, cache_dtype);
   NVS_REQUIRE(!is_code_dtype(cache_dtype) || (k_scale && v_scale), NVS_ERR_INVALID,
               "%s: quantised caches need k_scale and v_scale", who);
+  NVS_REQUIRE((int64_t)num_heads * q_head_stride < (1ll << 30) && (int64_t)num_heads * q_out_head_stride < (1ll << 30) &&
+                  (int64_t)num_kv_heads * (k_head_stride + v_head_stride + k_out_head_stride) < (1ll << 30),
+              NVS_ERR_INVALID, "%s: head strides too large", who);
   NVS_REQUIRE(q_tok_stride >= 0 && q_head_stride >= 0 && k_tok_stride >= 0 && k_head_stride >= 0 &&
                   v_tok_stride >= 0 && v_head_stride >= 0 && q_out_tok_stride >= 0 && q_out_head_stride >= 0 &&
                   k_out_tok_stride >= 0 && k_out_head_stride >= 0,
               NVS_ERR_INVALID, "%s: negative stride", who);
-  const int64_t units = num_tokens * (num_heads + 2 * (int64_t)num_kv_heads);
-  if (units == 0) return NVS_OK;
-  constexpr int kRowsPerBlock = kPrepThreads / kRowLanes;
-  const int64_t blocks = (units + kRowsPerBlock - 1) / kRowsPerBlock;
+  if (num_tokens == 0) return NVS_OK;
+  const int64_t blocks = (num_tokens + kPrepTokens - 1) / kPrepTokens;
   NVS_REQUIRE(blocks < (1ll << 31), NVS_ERR_INVALID, "%s: too many tokens (%lld)", who, (long long)num_tokens);
   PrepArgs a;
   a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v;
