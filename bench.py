@@ -12,7 +12,10 @@ sequences, new U[512, 4096] over 0-8 cached blocks, seed 2), quantised
 decode tokens/s (256 sequences, ctx U[1024, 4096], fp8 / int8 / bf16, seed
 3), the mixed chunked-prefill + decode step at a Qwen3-32B-like shape (seed
 4), the dominant kernel's roofline fraction (HIP events on the launch
-stream) and the CPU eager restatement timed on the host cores.
+stream), the CPU eager restatement timed on the host cores, and the steps
+either side of the path: the fused q/k norm + rotary + KV store
+(`qk_prep`), the step's Context built on the device (`step_context`) and
+the KV handoff block copies (`kv_handoff`).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--only decode|prefill|quant|mixed|prep|context|handoff]
 """
