@@ -230,9 +230,12 @@ int nvs_paged_attention(const void* q, int64_t q_tok_stride,
  * block_tables-is-None call of prefill_flashattn (reference
  * attention.py:338-354, flash_attn_varlen_func without block_table) and the
  * no-prefix branch of prefill_torch (attention.py:400-439).
- *   k, v          [num_tokens, num_kv_heads, head_dim] BF16 with strides;
+ *   q, out        [num_tokens, num_heads, head_dim] with strides.
+ *   k, v          [num_kv_tokens, num_kv_heads, head_dim] BF16 with strides;
  *                 keys of sequence i are rows cu_seqlens_k[i] ..
- *                 cu_seqlens_k[i+1]-1.  Same mask, GQA map, output and
+ *                 cu_seqlens_k[i+1]-1 (as flash_attn_varlen_func, the key
+ *                 rows need not match the query rows; reads are clamped to
+ *                 [0, num_kv_tokens)).  Same mask, GQA map, output and
  *                 workspace rule as nvs_paged_attention; head_dim 128.
  */
 int nvs_varlen_attention(const void* q, int64_t q_tok_stride,
@@ -241,12 +244,12 @@ int nvs_varlen_attention(const void* q, int64_t q_tok_stride,
                          int64_t v_tok_stride, int64_t v_head_stride,
                          const int32_t* cu_seqlens_q,
                          const int32_t* cu_seqlens_k, int num_seqs,
-                         int64_t num_tokens, int max_seqlen_q,
-                         int max_seqlen_k, int num_heads, int num_kv_heads,
-                         int head_dim, float softmax_scale, void* out,
-                         int64_t out_tok_stride, int64_t out_head_stride,
-                         void* workspace, int64_t workspace_bytes,
-                         void* stream);
+                         int64_t num_tokens, int64_t num_kv_tokens,
+                         int max_seqlen_q, int max_seqlen_k, int num_heads,
+                         int num_kv_heads, int head_dim, float softmax_scale,
+                         void* out, int64_t out_tok_stride,
+                         int64_t out_head_stride, void* workspace,
+                         int64_t workspace_bytes, void* stream);
 
 /*
  * Step metadata built on the device.  Replaces the per-token loops of

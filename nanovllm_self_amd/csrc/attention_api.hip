@@ -153,7 +153,7 @@ extern "C" int nvs_varlen_attention(const void* q, int64_t q_tok_stride, int64_t
                                     int64_t k_head_stride, int64_t v_tok_stride,
                                     int64_t v_head_stride, const int32_t* cu_seqlens_q,
                                     const int32_t* cu_seqlens_k, int num_seqs, int64_t num_tokens,
-                                    int max_seqlen_q, int max_seqlen_k, int num_heads,
+                                    int64_t num_kv_tokens, int max_seqlen_q, int max_seqlen_k, int num_heads,
                                     int num_kv_heads, int head_dim, float softmax_scale, void* out,
                                     int64_t out_tok_stride, int64_t out_head_stride,
                                     void* workspace, int64_t workspace_bytes, void* stream) {
@@ -165,10 +165,12 @@ extern "C" int nvs_varlen_attention(const void* q, int64_t q_tok_stride, int64_t
   P.v_ts = v_tok_stride; P.v_hs = v_head_stride;
   P.bt = nullptr;
   P.cu_q = cu_seqlens_q; P.cu_k = cu_seqlens_k;
-  P.B = num_seqs; P.T = num_tokens; P.max_seqlen_q = max_seqlen_q; P.max_seqlen_k = max_seqlen_k;
+  P.B = num_seqs; P.T = num_tokens; P.Tk = num_kv_tokens;
+  P.max_seqlen_q = max_seqlen_q; P.max_seqlen_k = max_seqlen_k;
   P.Hq = num_heads; P.Hkv = num_kv_heads; P.softmax_scale = softmax_scale;
   P.out = out; P.out_ts = out_tok_stride; P.out_hs = out_head_stride;
   if (num_seqs == 0 || num_tokens == 0) return NVS_OK;
+  NVS_REQUIRE(num_kv_tokens >= 1, NVS_ERR_INVALID, "varlen_attention: num_kv_tokens must be >= 1");
   int rc = validate_common(P, "varlen_attention");
   if (rc != NVS_OK) return rc;
   NVS_REQUIRE(head_dim == kHeadDim, NVS_ERR_UNSUPPORTED,

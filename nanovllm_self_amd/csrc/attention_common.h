@@ -163,7 +163,8 @@ struct AttnParams {
   const int32_t* cu_q;
   const int32_t* cu_k;
   int B;
-  int64_t T;
+  int64_t T;   // query / output rows
+  int64_t Tk;  // rows of the local k/v (varlen mode)
   int max_seqlen_q, max_seqlen_k;
   int Hq, Hkv;
   float softmax_scale;

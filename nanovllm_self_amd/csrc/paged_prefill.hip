@@ -58,7 +58,7 @@ struct PrefillArgs {
   const int32_t* bt;
   int bt_stride;  // row stride == number of columns
   int NB;
-  int64_t T;  // rows of the local k/v
+  int64_t T;  // rows of the local k/v (clamp bound of their reads)
   int bs;
   const uint16_t* k;
   const uint16_t* v;
@@ -485,7 +485,7 @@ int launch_prefill(const AttnParams& P, const Plan& plan, hipStream_t stream) {
   PrefillArgs a;
   a.q = (const uint16_t*)P.q; a.q_ts = P.q_ts; a.q_hs = P.q_hs;
   a.kc = P.kc; a.vc = P.vc; a.ks = P.ks; a.vs = P.vs;
-  a.bt = P.bt; a.bt_stride = (int)P.bt_stride; a.bs = P.bs; a.NB = (int)P.NB; a.T = P.T;
+  a.bt = P.bt; a.bt_stride = (int)P.bt_stride; a.bs = P.bs; a.NB = (int)P.NB; a.T = P.Tk;
   a.k = (const uint16_t*)P.k; a.v = (const uint16_t*)P.v;
   a.k_ts = P.k_ts; a.k_hs = P.k_hs; a.v_ts = P.v_ts; a.v_hs = P.v_hs;
   a.cu_q = P.cu_q; a.cu_k = P.cu_k;

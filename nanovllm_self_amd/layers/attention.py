@@ -284,7 +284,7 @@ class PagedAttention(nn.Module):
                 lib.nvs_varlen_attention(
                     q.data_ptr(), q.stride(0), q.stride(1),
                     k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1), v.stride(0), v.stride(1),
-                    cu_q.data_ptr(), cu_k.data_ptr(), B, T, max_q, max_k,
+                    cu_q.data_ptr(), cu_k.data_ptr(), B, T, k.shape[0], max_q, max_k,
                     self.num_heads, self.num_kv_heads, self.head_dim, scale,
                     out.data_ptr(), out.stride(0), out.stride(1), _lib.ptr(ws), ws_bytes, stream,
                 ),
@@ -470,6 +470,28 @@ class PagedAttention(nn.Module):
             context_lens=lens, block_tables=context.block_tables,
         )
         return self._attention(q, None, None, ctx)
+
+    def decode_attention_torch(self, q, k_batch, v_batch, kv_mask):
+        """Decode over gathered K/V (attention.py:586-675, an entry the
+        reference keeps but never calls): q [B, Hq, D], k_batch / v_batch
+        [B, max_len, Hkv, D] as get_kv_cache returns them, kv_mask
+        [B, max_len] True for a real key.  The kept keys are compacted
+        sequence by sequence (their order is irrelevant to the softmax) and
+        served by the varlen kernel, one query per sequence seeing every kept
+        key; a sequence with no key returns 0."""
+        B = q.shape[0]
+        dev = q.device
+        _need_device(q, "q")
+        mask = kv_mask.to(device=dev, dtype=torch.bool)
+        lens = mask.sum(dim=1, dtype=torch.int32)
+        cu_q = torch.arange(B + 1, dtype=torch.int32, device=dev)
+        cu_k = torch.zeros(B + 1, dtype=torch.int32, device=dev)
+        cu_k[1:] = torch.cumsum(lens, 0)
+        ctx = Context(
+            cu_seqlens_q=cu_q, cu_seqlens_k=cu_k, max_seqlen_q=1 if B else 0,
+            max_seqlen_k=int(lens.max().item()) if B else 0, context_lens=lens, block_tables=None,
+        )
+        return self._attention(q, k_batch[mask], v_batch[mask], ctx)
 
 
 # The name the attention layer goes by in the engine's documentation.

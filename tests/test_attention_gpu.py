@@ -335,3 +335,36 @@ def test_forward_profile_and_decode_entry(device):
     out2 = wl.attn.forward(wl.q, wl.k, wl.v, wl.context)
     torch.cuda.synchronize()
     assert torch.equal(out, out2)
+
+
+def test_decode_attention_torch_entry(device):
+    """decode_attention_torch (attention.py:586-675) over get_kv_cache's
+    gathered K/V equals the paged decode of the same batch; an arbitrary
+    mask (holes, an empty row) matches the oracle over the kept keys."""
+    say("decode_attention_torch")
+    wl = W.decode_small(device)
+    attn = wl.attn
+    paged = attn.forward(wl.q, wl.k, wl.v, wl.context)  # also stores the step's token
+    k_batch, v_batch, kv_mask = attn.get_kv_cache(wl.context)
+    got = attn.decode_attention_torch(wl.q, k_batch, v_batch, kv_mask)
+    torch.cuda.synchronize()
+    compare(bf16_to_np(got), bf16_to_np(paged), False, "decode_attention_torch vs paged decode")
+
+    g = torch.Generator().manual_seed(5)
+    B, Lmax, Hq, Hkv, D = 5, 300, 16, 8, 128
+    q = torch.randn(B, Hq, D, generator=g).to(torch.bfloat16)
+    kb = torch.randn(B, Lmax, Hkv, D, generator=g).to(torch.bfloat16)
+    vb = torch.randn(B, Lmax, Hkv, D, generator=g).to(torch.bfloat16)
+    mask = torch.rand(B, Lmax, generator=g) < 0.7
+    mask[1] = False  # no key: output 0
+    mask[2, 64:] = False  # a prefix
+    out = attn.decode_attention_torch(q.to(device), kb.to(device), vb.to(device), mask.to(device))
+    torch.cuda.synchronize()
+    ref = np.zeros((B, Hq, D), np.float32)
+    for b in range(B):
+        keep = mask[b]
+        if keep.any():
+            ref[b] = AO.attention_cached(q[b:b + 1].float(), kb[b:b + 1][:, keep].float(), vb[b:b + 1][:, keep].float(),
+                                         [0, 1], [0, int(keep.sum())], Hq, Hkv, D).numpy()[0]
+    compare(bf16_to_np(out), ref, False, "decode_attention_torch vs oracle")
+    assert np.all(bf16_to_np(out)[1] == 0)
