@@ -30,6 +30,7 @@ from nanovllm_self_amd import PagedAttention
 from nanovllm_self_amd.kv_cache import KVCacheConfig, SeqSlice, allocate_kv_cache, bind_kv_cache
 from oracle import attn_oracle as AO
 from oracle import prep_oracle as PO
+from oracle import kv_oracle as KO
 from oracle.kv_oracle import round_to_bf16
 from tests.gpu_util import bf16_to_np, compare, say
 
@@ -54,13 +55,15 @@ class Model:
 
 
 class Seq:
-    """The Sequence fields the runner reads, plus the oracle's per-sequence K/V."""
+    """The Sequence fields the runner reads, plus the oracle's per-sequence K/V
+    as the cache holds it (bf16 values, or the quantised codes' bf16(code *
+    scale))."""
 
     def __init__(self, tokens, blocks):
         self.tokens = list(tokens)
         self.block_table = list(blocks)
         self.num_cached_tokens = 0
-        self.k = np.zeros((0, HKV, D), np.float32)  # rotated k, bf16 values
+        self.k = np.zeros((0, HKV, D), np.float32)
         self.v = np.zeros((0, HKV, D), np.float32)
 
     def slice(self, n_new):
@@ -80,8 +83,22 @@ def gpu_step(model, attn, batch, device):
     return ctx, out
 
 
-def oracle_step(model, batch):
-    """The step on the CPU; extends each sequence's K/V as the store would."""
+def cached_values(x, kv):
+    """What the cache gives back for rows x (bf16 values): x itself, or the
+    per-token quantised codes dequantised and rounded to bf16."""
+    if kv == "bf16":
+        return x
+    quant = KO.quantize_int8_per_token if kv == "int8" else KO.quantize_fp8_per_token
+    codes, sc = quant(x)
+    return round_to_bf16(KO.dequantize_per_token(codes, sc, kv))
+
+
+def oracle_step(model, batch, kv="bf16"):
+    """The step on the CPU; extends each sequence's cached K/V as the store
+    would.  A step without block tables (no sequence has cached tokens)
+    attends over the raw k/v, the others over the cache (attention.py:
+    401-415 against 441-498)."""
+    fresh = all(s.num_cached_tokens == 0 for s, _ in batch)
     outs = []
     for s, n in batch:
         a = s.num_cached_tokens
@@ -89,10 +106,12 @@ def oracle_step(model, batch):
         pos = np.arange(a, a + n)
         q, k = PO.qk_norm_rope(bf16_to_np(model.eq[ids]), bf16_to_np(model.ek[ids]), pos, bf16_to_np(model.qw),
                                bf16_to_np(model.kw), EPS, model.table)
-        s.k = np.concatenate([s.k, k])
-        s.v = np.concatenate([s.v, bf16_to_np(model.ev[ids])])
-        kb, vb = torch.from_numpy(s.k)[None], torch.from_numpy(s.v)[None]
-        outs.append(AO.attention_cached(torch.from_numpy(q), kb, vb, [0, n], [0, len(s.k)], HQ, HKV, D).numpy())
+        v = bf16_to_np(model.ev[ids])
+        s.k = np.concatenate([s.k, cached_values(k, kv)])
+        s.v = np.concatenate([s.v, cached_values(v, kv)])
+        kk, vv = (k, v) if fresh else (s.k, s.v)
+        kb, vb = torch.from_numpy(np.ascontiguousarray(kk))[None], torch.from_numpy(np.ascontiguousarray(vv))[None]
+        outs.append(AO.attention_cached(torch.from_numpy(q), kb, vb, [0, n], [0, kb.shape[1]], HQ, HKV, D).numpy())
     return np.concatenate(outs)
 
 
@@ -103,12 +122,12 @@ def greedy(model, out_rows):
     return top.indices[:, 0].tolist(), (top.values[:, 0] - top.values[:, 1]).tolist(), logits
 
 
-def run_step(model, attn, batch, device, what):
+def run_step(model, attn, batch, device, what, kv="bf16"):
     say(what)
     ctx, out = gpu_step(model, attn, batch, device)
-    ref = oracle_step(model, batch)
+    ref = oracle_step(model, batch, kv)
     got = bf16_to_np(out)
-    compare(got, ref, False, what)
+    compare(got, ref, kv != "bf16", what)
     last = np.cumsum([n for _, n in batch]) - 1
     want, margin, _ = greedy(model, round_to_bf16(ref[last]))
     mine, _, _ = greedy(model, got[last])
@@ -122,19 +141,23 @@ def run_step(model, attn, batch, device, what):
     return ctx, got, ref
 
 
-def test_generation_loop_with_prefix_hit_and_mixed_steps(device):
+CACHE = {"bf16": (torch.bfloat16, "none"), "fp8": (torch.float8_e4m3fn, "fp8_e4m3"), "int8": (torch.int8, "int8_mock")}
+
+
+@pytest.mark.parametrize("kv", ["bf16", "fp8", "int8"])
+def test_generation_loop_with_prefix_hit_and_mixed_steps(device, kv):
     model = Model(device)
-    cfg = KVCacheConfig(dtype=torch.bfloat16, kv_cache_dtype=torch.bfloat16, attention_compute_dtype=torch.bfloat16,
-                        block_size=BS, num_blocks=NB)
+    cfg = KVCacheConfig(dtype=torch.bfloat16, kv_cache_dtype=CACHE[kv][0], attention_compute_dtype=torch.bfloat16,
+                        kv_cache_quant_mode=CACHE[kv][1], block_size=BS, num_blocks=NB)
     attn = PagedAttention(HQ, HKV, D, dtype=torch.bfloat16)
-    kv, sc = allocate_kv_cache(1, HKV, D, cfg, device)
-    bind_kv_cache([attn], kv, sc, cfg)
+    kv_cache, scales = allocate_kv_cache(1, HKV, D, cfg, device)
+    bind_kv_cache([attn], kv_cache, scales, cfg)
     rng = np.random.default_rng(7)
     prompt_a = rng.integers(0, V, 300).tolist()
 
     # A: a fresh 300-token prompt (no cached tokens anywhere: block_tables None).
     a = Seq(prompt_a, [3, 9])
-    ctx, _, _ = run_step(model, attn, [(a, 300)], device, "engine: prefill A (fresh)")
+    ctx, _, _ = run_step(model, attn, [(a, 300)], device, f"engine {kv}: prefill A (fresh)", kv)
     assert ctx.block_tables is None
 
     # B: A's first 300 tokens plus 100 more; the first full block is a cache
@@ -144,17 +167,17 @@ def test_generation_loop_with_prefix_hit_and_mixed_steps(device):
     b.num_cached_tokens = shared // BS * BS
     assert b.num_cached_tokens == 256
     b.k, b.v = a.k[:256].copy(), a.v[:256].copy()  # the oracle's view of the shared block
-    ctx, out_b, _ = run_step(model, attn, [(b, len(b.tokens) - 256)], device, "engine: prefill B over a cached block")
+    ctx, out_b, _ = run_step(model, attn, [(b, len(b.tokens) - 256)], device, f"engine {kv}: prefill B over a cached block", kv)
     assert ctx.block_tables is not None and int(ctx.cu_seqlens_k[-1]) > int(ctx.cu_seqlens_q[-1])
     assert int(ctx.cu_seqlens_q[-1]) == 144
 
     # C: B's 400 prompt tokens as a fresh sequence, prefilled in two chunks
     # beside decode steps of A and B (mixed batches).
     c = Seq(b.tokens[:400], [11, 12])
-    run_step(model, attn, [(a, 1), (b, 1), (c, 256)], device, "engine: decode A, B + chunk 1 of C")
-    _, out_c, _ = run_step(model, attn, [(a, 1), (c, 144), (b, 1)], device, "engine: decode A, chunk 2 of C, decode B")
+    run_step(model, attn, [(a, 1), (b, 1), (c, 256)], device, f"engine {kv}: decode A, B + chunk 1 of C", kv)
+    _, out_c, _ = run_step(model, attn, [(a, 1), (c, 144), (b, 1)], device, f"engine {kv}: decode A, chunk 2 of C, decode B", kv)
     # C's last prompt row attends over the same 400 keys as B's last prompt row.
-    np.testing.assert_allclose(out_c[1 + 143], out_b[143], rtol=0, atol=2e-2)
+    np.testing.assert_allclose(out_c[1 + 143], out_b[143], rtol=0, atol=2e-2 if kv == "bf16" else 5e-2)
     for step in range(6):
-        run_step(model, attn, [(a, 1), (b, 1), (c, 1)], device, f"engine: decode step {step} of A, B, C")
+        run_step(model, attn, [(a, 1), (b, 1), (c, 1)], device, f"engine {kv}: decode step {step} of A, B, C", kv)
     assert len(a.tokens) == 300 + 9 and len(c.tokens) == 400 + 7
