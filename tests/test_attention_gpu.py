@@ -368,3 +368,30 @@ def test_decode_attention_torch_entry(device):
                                          [0, 1], [0, int(keep.sum())], Hq, Hkv, D).numpy()[0]
     compare(bf16_to_np(out), ref, False, "decode_attention_torch vs oracle")
     assert np.all(bf16_to_np(out)[1] == 0)
+
+
+@pytest.mark.parametrize("kv", ["bf16", "fp8"])
+def test_determinism_and_batch_split(device, kv):
+    """The same call twice gives the same bits (split rows are merged in a
+    fixed order), and a sequence's output does not depend on the batch it is
+    in: the mixed batch's two halves attended on their own match the whole
+    batch's rows (the stream-K split points move, so within the bars)."""
+    from nanovllm_self_amd.kv_cache import build_context
+
+    say(f"determinism + batch split {kv}")
+    wl = W.mixed_32b(device, kv=kv, n_decode=24, n_chunks=2, chunk=384)
+    attn, ctx = wl.attn, wl.context
+    first = attn.forward(wl.q, wl.k, wl.v, ctx)
+    again = attn.prefill_flashattn(wl.q, wl.k, wl.v, ctx)
+    torch.cuda.synchronize()
+    assert torch.equal(first, again), "two identical calls differ"
+    full = bf16_to_np(first)
+    cu = ctx.cu_seqlens_q.cpu().tolist()
+    n = len(wl.seqs)
+    for part in (list(range(0, n, 2)), list(range(1, n, 2))):  # interleaved halves: decode and prefill rows in both
+        sub = build_context([wl.seqs[i] for i in part], wl.block_size, device)
+        rows = np.concatenate([np.arange(cu[i], cu[i + 1]) for i in part])
+        idx = torch.as_tensor(rows, device=device)
+        out = attn.prefill_flashattn(wl.q[idx], wl.k[idx], wl.v[idx], sub)
+        torch.cuda.synchronize()
+        compare(bf16_to_np(out), full[rows], kv != "bf16", f"batch half {part[:3]}... vs whole batch ({kv})")
