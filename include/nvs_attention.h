@@ -226,6 +226,32 @@ int nvs_paged_attention(const void* q, int64_t q_tok_stride,
                         int64_t workspace_bytes, void* stream);
 
 /*
+ * The layer's forward in one call: the KV-cache write of the step's k / v
+ * (as nvs_store_kvcache) and then the attention (as nvs_paged_attention).
+ * Replaces PagedAttention.forward_unified's write_kv_cache(k, v,
+ * slot_mapping) + prefill_flashattn(q, k, v, context) (reference
+ * attention.py:500-546).  When every row is a decode row (max_seqlen_q ==
+ * 1), the cache and the sources are BF16 and the rows 16-byte aligned, the
+ * decode kernel writes each row's new token itself before it reads the row's
+ * last tile (one launch fewer); otherwise the store kernel runs first.  The
+ * cache contents and the output equal the two calls made one after the
+ * other.
+ */
+int nvs_paged_attention_store(const void* q, int64_t q_tok_stride, int64_t q_head_stride,
+                              const void* k, const void* v, int src_dtype,
+                              int64_t k_tok_stride, int64_t k_head_stride,
+                              int64_t v_tok_stride, int64_t v_head_stride,
+                              const int32_t* slot_mapping, void* k_cache, void* v_cache,
+                              int cache_dtype, float* k_scale, float* v_scale,
+                              const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                              const int32_t* block_tables, int64_t bt_stride, int num_seqs,
+                              int64_t num_tokens, int max_seqlen_q, int max_seqlen_k,
+                              int num_heads, int num_kv_heads, int head_dim, int block_size,
+                              int64_t num_blocks, float softmax_scale, void* out,
+                              int64_t out_tok_stride, int64_t out_head_stride,
+                              void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
  * Causal varlen attention over the step's own (not cached) K/V: the
  * block_tables-is-None call of prefill_flashattn (reference
  * attention.py:338-354, flash_attn_varlen_func without block_table) and the

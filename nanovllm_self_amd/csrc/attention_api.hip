@@ -89,18 +89,18 @@ static int check_workspace(const AttnParams& P, const char* who) {
   return NVS_OK;
 }
 
-extern "C" int nvs_paged_attention(const void* q, int64_t q_tok_stride, int64_t q_head_stride,
-                                   const void* k_cache, const void* v_cache, int cache_dtype,
-                                   const float* k_scale, const float* v_scale,
-                                   const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
-                                   const int32_t* block_tables, int64_t bt_stride, int num_seqs,
-                                   int64_t num_tokens, int max_seqlen_q, int max_seqlen_k,
-                                   int num_heads, int num_kv_heads, int head_dim, int block_size,
-                                   int64_t num_blocks, float softmax_scale, void* out,
-                                   int64_t out_tok_stride, int64_t out_head_stride,
-                                   void* workspace, int64_t workspace_bytes, void* stream) {
-  clear_error();
-  AttnParams P = {};
+// nvs_paged_attention's body; P.kn != null asks the decode kernel to store
+// the step's new tokens itself (bf16 cache, decode rows only).
+static int paged_attention_impl(AttnParams& P, const void* q, int64_t q_tok_stride, int64_t q_head_stride,
+                                const void* k_cache, const void* v_cache, int cache_dtype,
+                                const float* k_scale, const float* v_scale,
+                                const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                                const int32_t* block_tables, int64_t bt_stride, int num_seqs,
+                                int64_t num_tokens, int max_seqlen_q, int max_seqlen_k,
+                                int num_heads, int num_kv_heads, int head_dim, int block_size,
+                                int64_t num_blocks, float softmax_scale, void* out,
+                                int64_t out_tok_stride, int64_t out_head_stride,
+                                void* workspace, int64_t workspace_bytes, void* stream) {
   P.q = q; P.q_ts = q_tok_stride; P.q_hs = q_head_stride;
   P.kc = k_cache; P.vc = v_cache; P.cache_dtype = cache_dtype; P.ks = k_scale; P.vs = v_scale;
   P.bt = block_tables; P.bt_stride = bt_stride; P.bs = block_size; P.NB = num_blocks;
@@ -146,6 +146,62 @@ extern "C" int nvs_paged_attention(const void* q, int64_t q_tok_stride, int64_t 
   rc = launch_plan(P, plan, /*paged=*/true, s);
   if (rc != NVS_OK) return rc;
   return launch_prefill(P, plan, s);
+}
+
+extern "C" int nvs_paged_attention(const void* q, int64_t q_tok_stride, int64_t q_head_stride,
+                                   const void* k_cache, const void* v_cache, int cache_dtype,
+                                   const float* k_scale, const float* v_scale,
+                                   const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                                   const int32_t* block_tables, int64_t bt_stride, int num_seqs,
+                                   int64_t num_tokens, int max_seqlen_q, int max_seqlen_k,
+                                   int num_heads, int num_kv_heads, int head_dim, int block_size,
+                                   int64_t num_blocks, float softmax_scale, void* out,
+                                   int64_t out_tok_stride, int64_t out_head_stride,
+                                   void* workspace, int64_t workspace_bytes, void* stream) {
+  clear_error();
+  AttnParams P = {};
+  return paged_attention_impl(P, q, q_tok_stride, q_head_stride, k_cache, v_cache, cache_dtype, k_scale, v_scale,
+                              cu_seqlens_q, cu_seqlens_k, block_tables, bt_stride, num_seqs, num_tokens,
+                              max_seqlen_q, max_seqlen_k, num_heads, num_kv_heads, head_dim, block_size,
+                              num_blocks, softmax_scale, out, out_tok_stride, out_head_stride, workspace,
+                              workspace_bytes, stream);
+}
+
+extern "C" int nvs_paged_attention_store(const void* q, int64_t q_tok_stride, int64_t q_head_stride,
+                                         const void* k, const void* v, int src_dtype, int64_t k_tok_stride,
+                                         int64_t k_head_stride, int64_t v_tok_stride, int64_t v_head_stride,
+                                         const int32_t* slot_mapping, void* k_cache, void* v_cache,
+                                         int cache_dtype, float* k_scale, float* v_scale,
+                                         const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                                         const int32_t* block_tables, int64_t bt_stride, int num_seqs,
+                                         int64_t num_tokens, int max_seqlen_q, int max_seqlen_k,
+                                         int num_heads, int num_kv_heads, int head_dim, int block_size,
+                                         int64_t num_blocks, float softmax_scale, void* out,
+                                         int64_t out_tok_stride, int64_t out_head_stride,
+                                         void* workspace, int64_t workspace_bytes, void* stream) {
+  clear_error();
+  AttnParams P = {};
+  // A batch of decode rows over a bf16 cache: the decode kernel stores the
+  // new tokens itself (one launch less).  Otherwise the store kernel first.
+  const bool fused = num_tokens > 0 && max_seqlen_q == 1 && cache_dtype == NVS_DTYPE_BF16 &&
+                     src_dtype == NVS_DTYPE_BF16 && k && v && slot_mapping && head_dim == kHeadDim &&
+                     k_tok_stride % 8 == 0 && k_head_stride % 8 == 0 && v_tok_stride % 8 == 0 &&
+                     v_head_stride % 8 == 0 && ((uintptr_t)k % 16) == 0 && ((uintptr_t)v % 16) == 0 &&
+                     k_tok_stride >= 0 && k_head_stride >= 0 && v_tok_stride >= 0 && v_head_stride >= 0;
+  if (fused) {
+    P.kn = k; P.vn = v; P.slots = slot_mapping;
+    P.kn_ts = k_tok_stride; P.kn_hs = k_head_stride; P.vn_ts = v_tok_stride; P.vn_hs = v_head_stride;
+  } else {
+    const int rc = nvs_store_kvcache(k, v, src_dtype, k_tok_stride, k_head_stride, v_tok_stride, v_head_stride,
+                                     slot_mapping, num_tokens, k_cache, v_cache, cache_dtype, k_scale, v_scale,
+                                     num_blocks, block_size, num_kv_heads, head_dim, stream);
+    if (rc != NVS_OK) return rc;
+  }
+  return paged_attention_impl(P, q, q_tok_stride, q_head_stride, k_cache, v_cache, cache_dtype, k_scale, v_scale,
+                              cu_seqlens_q, cu_seqlens_k, block_tables, bt_stride, num_seqs, num_tokens,
+                              max_seqlen_q, max_seqlen_k, num_heads, num_kv_heads, head_dim, block_size,
+                              num_blocks, softmax_scale, out, out_tok_stride, out_head_stride, workspace,
+                              workspace_bytes, stream);
 }
 
 extern "C" int nvs_varlen_attention(const void* q, int64_t q_tok_stride, int64_t q_head_stride,

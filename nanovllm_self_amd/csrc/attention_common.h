@@ -163,6 +163,12 @@ struct AttnParams {
   const int32_t* cu_q;
   const int32_t* cu_k;
   int B;
+  // The step's new k / v rows (bf16) that the decode kernel stores into a
+  // bf16 cache itself (null: the caller stored them).
+  const void* kn;
+  const void* vn;
+  int64_t kn_ts, kn_hs, vn_ts, vn_hs;
+  const int32_t* slots;
   int64_t T;   // query / output rows
   int64_t Tk;  // rows of the local k/v (varlen mode)
   int max_seqlen_q, max_seqlen_k;

@@ -50,6 +50,12 @@ struct DecodeArgs {
   float* ws_o;   // [max_waves, 2 slots, g, 128]
   float* ws_ml;  // [max_waves, 2 slots, g, 2]
   int32_t* ws_rec;  // [4 + 4 waves]: (T, Kw), then per wave the split row it merges
+  // New tokens stored by the decode waves themselves (bf16 cache; kn null: none).
+  const uint16_t* kn;
+  const uint16_t* vn;
+  int64_t kn_ts, kn_hs, vn_ts, vn_hs;
+  const int32_t* slots;
+  int64_t total_slots;
   const int32_t* cu_q;
   const int32_t* cu_k;
   int B;
@@ -427,6 +433,25 @@ __device__ __forceinline__ int wave_incl_scan(int v) {
   return v;
 }
 
+// The step's new token of a decode row (query row q0), kv head h, copied
+// into a bf16 cache at slot_mapping[q0] by the wave that owns the row's last
+// tile, before that wave loads anything: lanes 0-15 move the k row, lanes
+// 16-31 the v row, 16 bytes each.  The two rows' cache lines belong to this
+// (slot, head) alone, so the wave's own later loads of the tile see them once
+// the stores have completed.  Slots outside the cache are skipped, as the
+// store kernel skips them.
+__device__ __forceinline__ void store_new_token(const DecodeArgs& a, int q0, int h) {
+  const int lane = threadIdx.x & 63;
+  const int64_t slot = a.slots[q0];
+  if (slot < 0 || slot >= a.total_slots || lane >= 32) return;
+  const uint32_t off = lane_off(8u * (uint32_t)(lane & 15) * 2u);
+  const bool isv = lane >= 16;
+  const char* src = (const char*)(isv ? a.vn + (int64_t)q0 * a.vn_ts + (int64_t)h * a.vn_hs
+                                      : a.kn + (int64_t)q0 * a.kn_ts + (int64_t)h * a.kn_hs);
+  char* dst = (char*)(isv ? a.vc : a.kc) + (slot * a.Hkv + h) * (int64_t)(kHeadDim * 2);
+  *reinterpret_cast<u32x4*>(dst + off) = *reinterpret_cast<const u32x4*>(src + off);
+}
+
 // Zeroes the output of the round's decode rows that see no key (row b by
 // wave b % gridDim.x): no tile covers them, so no wave writes them otherwise.
 __device__ __forceinline__ void zero_keyless_rows(const DecodeArgs& a, const ScanRound& rd) {
@@ -444,6 +469,9 @@ __device__ __forceinline__ void zero_keyless_rows(const DecodeArgs& a, const Sca
         const int hq = x / (kHeadDim / 8), d = 8 * (x % (kHeadDim / 8));
         *reinterpret_cast<u32x4*>(a.out + (int64_t)q0 * a.out_ts + (int64_t)hq * a.out_hs + d) = u32x4{0, 0, 0, 0};
       }
+      // No tile covers this row, so its new token is stored here.
+      if (a.kn)
+        for (int h = 0; h < a.Hkv; ++h) store_new_token(a, q0, h);
     }
   }
 }
@@ -683,6 +711,32 @@ void paged_decode_kernel(DecodeArgs a, const int32_t* __restrict__ bt, const int
     n[j] = n[j - 1];
     if (left > j) advance(n[j]);
   }
+  // The new tokens of the rows whose last tile lies in this range are
+  // written by this wave (bf16 cache, a.kn set): a row ending inside the
+  // tiles the ring loads first is written before those loads, the others
+  // right after them, so the writes overlap the first loads; a fence then
+  // completes them before any later load is issued.  A wave that wrote
+  // nothing skips the fence (it would wait for the first loads).
+  Cursor sc_c = n[0];
+  int sc_tile = s0;  // global index of sc_c's tile
+  bool sc_more = KV == NVS_DTYPE_BF16 && a.kn != nullptr;
+  auto store_rows = [&](int below) {  // rows whose last tile is < below; true if any
+    bool any = false;
+    while (sc_more) {
+      const int last = sc_tile + (sc_c.n - 1 - sc_c.t);
+      if (last >= s0 + left) { sc_more = false; break; }  // the row ends in a later group's range
+      if (last >= below) break;
+      store_new_token(a, sc_c.q0, h);
+      any = true;
+      sc_tile = last + 1;
+      if (sc_tile >= s0 + left) { sc_more = false; break; }
+      next_row(a, cu_q, cu_k, sc_c);
+    }
+    return any;
+  };
+  if constexpr (KV == NVS_DTYPE_BF16) {
+    if (a.kn && store_rows(s0 + D - 1)) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  }
 
   bf16x8 qop[4];
   load_q<KV>(qop, a, n[0].q0, h, col, grp);
@@ -696,6 +750,9 @@ void paged_decode_kernel(DecodeArgs a, const int32_t* __restrict__ bt, const int
   DecodeTile<KV> r[D];
 #pragma unroll
   for (int j = 0; j < D - 1; ++j) decode_load<KV>(r[j], a, lo, tile_block(a, bt, n[j]), n[j].koff, h);
+  if constexpr (KV == NVS_DTYPE_BF16) {
+    if (a.kn && store_rows(s0 + left)) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  }
   int blk_last = tile_block(a, bt, n[D - 1]);
 
   // Tile i (cursor n[0]) from ring slot cur; the loads of tile i + D - 1 go
@@ -828,6 +885,9 @@ int launch_decode(const AttnParams& P, int max_waves, int waves, void* partials,
   a.Hq = P.Hq; a.Hkv = P.Hkv; a.g = P.Hq / P.Hkv; a.bs = P.bs;
   a.scale_log2 = P.softmax_scale * 1.4426950408889634f;
   a.cu_q = P.cu_q; a.cu_k = P.cu_k; a.B = P.B; a.T = P.T;
+  a.kn = (const uint16_t*)P.kn; a.vn = (const uint16_t*)P.vn;
+  a.kn_ts = P.kn_ts; a.kn_hs = P.kn_hs; a.vn_ts = P.vn_ts; a.vn_hs = P.vn_hs;
+  a.slots = P.slots; a.total_slots = P.NB * (int64_t)P.bs;
   a.out = (uint16_t*)P.out; a.out_ts = P.out_ts; a.out_hs = P.out_hs;
   a.ws_o = (float*)partials;
   a.ws_ml = a.ws_o + (int64_t)max_waves * 2 * a.g * kHeadDim;

@@ -253,8 +253,10 @@ class PagedAttention(nn.Module):
         return k_batch, v_batch, kv_mask
 
     # -------------------------------------------------------------- attention
-    def _attention(self, q, k, v, context):
-        """One call of the HIP attention over the whole (mixed) batch."""
+    def _attention(self, q, k, v, context, store_slots=None):
+        """One call of the HIP attention over the whole (mixed) batch; with
+        store_slots the same call first writes k / v to those cache slots
+        (nvs_paged_attention_store, paged mode only)."""
         compute = torch.bfloat16
         if q.dtype != compute:
             q = q.to(compute)
@@ -306,17 +308,33 @@ class PagedAttention(nn.Module):
             if bt.dtype != torch.int32 or not bt.is_contiguous():
                 bt = bt.to(torch.int32).contiguous()
             num_blocks, block_size = kc.shape[0], kc.shape[1]
-            _lib.check(
-                lib.nvs_paged_attention(
-                    q.data_ptr(), q.stride(0), q.stride(1),
-                    kc.data_ptr(), vc.data_ptr(), _lib.nvs_dtype(kc.dtype), _lib.ptr(ks), _lib.ptr(vs),
-                    cu_q.data_ptr(), cu_k.data_ptr(), bt.data_ptr(), bt.size(1),
-                    B, T, max_q, max_k, self.num_heads, self.num_kv_heads, self.head_dim,
-                    block_size, num_blocks, scale, out.data_ptr(), out.stride(0), out.stride(1),
-                    _lib.ptr(ws), ws_bytes, stream,
-                ),
-                "paged_attention",
-            )
+            if store_slots is None:
+                _lib.check(
+                    lib.nvs_paged_attention(
+                        q.data_ptr(), q.stride(0), q.stride(1),
+                        kc.data_ptr(), vc.data_ptr(), _lib.nvs_dtype(kc.dtype), _lib.ptr(ks), _lib.ptr(vs),
+                        cu_q.data_ptr(), cu_k.data_ptr(), bt.data_ptr(), bt.size(1),
+                        B, T, max_q, max_k, self.num_heads, self.num_kv_heads, self.head_dim,
+                        block_size, num_blocks, scale, out.data_ptr(), out.stride(0), out.stride(1),
+                        _lib.ptr(ws), ws_bytes, stream,
+                    ),
+                    "paged_attention",
+                )
+            else:
+                slots = store_slots.to(torch.int32).contiguous()
+                _lib.check(
+                    lib.nvs_paged_attention_store(
+                        q.data_ptr(), q.stride(0), q.stride(1),
+                        k.data_ptr(), v.data_ptr(), _lib.nvs_dtype(k.dtype), k.stride(0), k.stride(1),
+                        v.stride(0), v.stride(1), slots.data_ptr(),
+                        kc.data_ptr(), vc.data_ptr(), _lib.nvs_dtype(kc.dtype), _lib.ptr(ks), _lib.ptr(vs),
+                        cu_q.data_ptr(), cu_k.data_ptr(), bt.data_ptr(), bt.size(1),
+                        B, T, max_q, max_k, self.num_heads, self.num_kv_heads, self.head_dim,
+                        block_size, num_blocks, scale, out.data_ptr(), out.stride(0), out.stride(1),
+                        _lib.ptr(ws), ws_bytes, stream,
+                    ),
+                    "paged_attention_store",
+                )
         return out if self.dtype == compute else out.to(self.dtype)
 
     def prefill(self, q, k, v, context):
@@ -349,10 +367,36 @@ class PagedAttention(nn.Module):
         cached (dequantised) K/V with the bottom-right causal mask."""
         return self._attention(q, k, v, context)
 
+    def _store_in_decode(self, k, v, context) -> bool:
+        """True when the write of a decode batch can ride in the decode
+        kernel: bf16 cache and sources, every row a decode row, and neither
+        write_kv_cache nor store_kv_cache_torch replaced on this layer (the
+        reference's experiments wrap them per instance, and then they must
+        run)."""
+        cls = type(self)
+        return (
+            "write_kv_cache" not in self.__dict__ and "store_kv_cache_torch" not in self.__dict__
+            and cls.write_kv_cache is PagedAttention.write_kv_cache
+            and cls.store_kv_cache_torch is PagedAttention.store_kv_cache_torch
+            and self.kv_writer_backend in ("torch", "hip")
+            and self.forward_backend in ("flashattn", "hip", "torch")
+            and context.block_tables is not None and int(context.max_seqlen_q) == 1
+            and self.kv_cache_quant_mode == "none" and self.attention_compute_dtype == torch.bfloat16
+            and self.k_cache is not None and self.k_cache.dtype == torch.bfloat16
+            and self.v_cache is not None and self.v_cache.dtype == torch.bfloat16
+            and self.k_cache.is_contiguous() and self.v_cache.is_contiguous()
+            and k.dtype == torch.bfloat16 and v.dtype == torch.bfloat16 and k.is_cuda and v.is_cuda
+            and k.stride(-1) == 1 and v.stride(-1) == 1
+        )
+
     def forward_unified(self, q, k, v, context):
         """Write the step's K/V, then one attention call over the whole batch
-        (attention.py:500-546)."""
+        (attention.py:500-546).  A decode batch over a bf16 cache does both in
+        one call: the decode kernel writes each row's new token before reading
+        its last tile."""
         should_profile = self._should_profile()
+        if not should_profile and self._store_in_decode(k, v, context):
+            return self._attention(q, k, v, context, store_slots=context.slot_mapping)
         if should_profile:
             torch.cuda.synchronize()
             t0 = perf_counter()

@@ -395,3 +395,54 @@ def test_determinism_and_batch_split(device, kv):
         out = attn.prefill_flashattn(wl.q[idx], wl.k[idx], wl.v[idx], sub)
         torch.cuda.synchronize()
         compare(bf16_to_np(out), full[rows], kv != "bf16", f"batch half {part[:3]}... vs whole batch ({kv})")
+
+
+def _cache_bytes(attn):
+    return (attn.k_cache.view(torch.uint8).clone(), attn.v_cache.view(torch.uint8).clone())
+
+
+@pytest.mark.parametrize("which", ["decode_small", "decode_8b"])
+def test_decode_store_in_kernel_equals_store_then_attend(device, which):
+    """forward on a decode batch over a bf16 cache writes the new tokens
+    inside the decode kernel; the cache bytes and the output equal
+    write_kv_cache followed by the attention call, bit for bit."""
+    say(f"store in the decode kernel: {which}")
+    a, b = W.BUILDERS[which](device), W.BUILDERS[which](device)  # identical seeded workloads
+    assert a.attn._store_in_decode(a.k, a.v, a.context)
+    fused = a.attn.forward(a.q, a.k, a.v, a.context)
+    b.attn.write_kv_cache(b.k, b.v, b.context.slot_mapping)
+    plain = b.attn.prefill_flashattn(b.q, b.k, b.v, b.context)
+    torch.cuda.synchronize()
+    assert torch.equal(fused, plain)
+    for x, y in zip(_cache_bytes(a.attn), _cache_bytes(b.attn)):
+        assert torch.equal(x, y), "cache contents differ"
+
+
+def test_decode_store_in_kernel_edge_rows(device):
+    """A decode row with no visible key still has its token written; a
+    negative slot is skipped; a wrapped write_kv_cache is still called."""
+    say("store in the decode kernel: keyless row, skipped slot, wrapped writer")
+    tabs = _tables([300, 40, 90], 8, 21)
+    seqs = [SeqSlice(tabs[0], 299, 1), SeqSlice(tabs[1], 39, 1), SeqSlice(tabs[2], 89, 1)]
+    a, b = _custom(seqs, 8, 2, 8, seed=22), _custom(seqs, 8, 2, 8, seed=22)
+    for wl in (a, b):
+        # Row 1 sees no key (k_len 0); row 2's slot is -1.
+        ctx = wl.context
+        ctx.cu_seqlens_k = torch.tensor([0, 300, 300, 390], dtype=torch.int32, device=device)
+        ctx.context_lens = torch.tensor([300, 0, 90], dtype=torch.int32, device=device)
+        ctx.slot_mapping = ctx.slot_mapping.clone()
+        ctx.slot_mapping[2] = -1
+    fused = a.attn.forward(a.q, a.k, a.v, a.context)
+    b.attn.write_kv_cache(b.k, b.v, b.context.slot_mapping)
+    plain = b.attn.prefill_flashattn(b.q, b.k, b.v, b.context)
+    torch.cuda.synchronize()
+    assert torch.equal(fused, plain) and torch.all(fused[1] == 0)
+    for x, y in zip(_cache_bytes(a.attn), _cache_bytes(b.attn)):
+        assert torch.equal(x, y), "cache contents differ"
+    calls = []
+    inner = a.attn.write_kv_cache
+    a.attn.write_kv_cache = lambda k, v, s: (calls.append(1), inner(k, v, s))[1]
+    assert not a.attn._store_in_decode(a.k, a.v, a.context)
+    again = a.attn.forward(a.q, a.k, a.v, a.context)
+    torch.cuda.synchronize()
+    assert calls == [1] and torch.equal(again, fused)
