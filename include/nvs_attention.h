@@ -231,9 +231,10 @@ int nvs_paged_attention(const void* q, int64_t q_tok_stride,
  * Replaces PagedAttention.forward_unified's write_kv_cache(k, v,
  * slot_mapping) + prefill_flashattn(q, k, v, context) (reference
  * attention.py:500-546).  When every row is a decode row (max_seqlen_q ==
- * 1), the cache and the sources are BF16 and the rows 16-byte aligned, the
- * decode kernel writes each row's new token itself before it reads the row's
- * last tile (one launch fewer); otherwise the store kernel runs first.  The
+ * 1), the sources are BF16 and the rows 16-byte aligned, the decode kernel
+ * writes each row's new token itself (BF16 values, or fp8 / int8 codes and
+ * their scales) before it reads the row's last tile (one launch fewer);
+ * otherwise the store kernel runs first.  The
  * cache contents and the output equal the two calls made one after the
  * other.
  */

@@ -90,7 +90,7 @@ static int check_workspace(const AttnParams& P, const char* who) {
 }
 
 // nvs_paged_attention's body; P.kn != null asks the decode kernel to store
-// the step's new tokens itself (bf16 cache, decode rows only).
+// the step's new tokens itself (decode rows only).
 static int paged_attention_impl(AttnParams& P, const void* q, int64_t q_tok_stride, int64_t q_head_stride,
                                 const void* k_cache, const void* v_cache, int cache_dtype,
                                 const float* k_scale, const float* v_scale,
@@ -181,9 +181,12 @@ extern "C" int nvs_paged_attention_store(const void* q, int64_t q_tok_stride, in
                                          void* workspace, int64_t workspace_bytes, void* stream) {
   clear_error();
   AttnParams P = {};
-  // A batch of decode rows over a bf16 cache: the decode kernel stores the
-  // new tokens itself (one launch less).  Otherwise the store kernel first.
-  const bool fused = num_tokens > 0 && max_seqlen_q == 1 && cache_dtype == NVS_DTYPE_BF16 &&
+  // A batch of decode rows with bf16 sources: the decode kernel stores the
+  // new tokens itself (one launch less), values into a bf16 cache, codes and
+  // scales into an fp8 / int8 one.  Otherwise the store kernel first.
+  const bool cache_ok = cache_dtype == NVS_DTYPE_BF16 ||
+                        ((cache_dtype == NVS_DTYPE_FP8_E4M3 || cache_dtype == NVS_DTYPE_INT8) && k_scale && v_scale);
+  const bool fused = num_tokens > 0 && max_seqlen_q == 1 && cache_ok &&
                      src_dtype == NVS_DTYPE_BF16 && k && v && slot_mapping && head_dim == kHeadDim &&
                      k_tok_stride % 8 == 0 && k_head_stride % 8 == 0 && v_tok_stride % 8 == 0 &&
                      v_head_stride % 8 == 0 && ((uintptr_t)k % 16) == 0 && ((uintptr_t)v % 16) == 0 &&

@@ -33,6 +33,7 @@
 
 #include "nvs_common.h"
 #include "attention_common.h"
+#include "store_common.h"
 
 namespace nvs {
 
@@ -50,7 +51,9 @@ struct DecodeArgs {
   float* ws_o;   // [max_waves, 2 slots, g, 128]
   float* ws_ml;  // [max_waves, 2 slots, g, 2]
   int32_t* ws_rec;  // [4 + 4 waves]: (T, Kw), then per wave the split row it merges
-  // New tokens stored by the decode waves themselves (bf16 cache; kn null: none).
+  // New tokens (bf16) stored by the decode waves themselves: copied into a
+  // bf16 cache, quantised per token and kv head into an fp8 / int8 one with
+  // their scales into ks / vs (kn null: none).
   const uint16_t* kn;
   const uint16_t* vn;
   int64_t kn_ts, kn_hs, vn_ts, vn_hs;
@@ -433,27 +436,43 @@ __device__ __forceinline__ int wave_incl_scan(int v) {
   return v;
 }
 
-// The step's new token of a decode row (query row q0), kv head h, copied
-// into a bf16 cache at slot_mapping[q0] by the wave that owns the row's last
-// tile, before that wave loads anything: lanes 0-15 move the k row, lanes
-// 16-31 the v row, 16 bytes each.  The two rows' cache lines belong to this
-// (slot, head) alone, so the wave's own later loads of the tile see them once
-// the stores have completed.  Slots outside the cache are skipped, as the
-// store kernel skips them.
+// The step's new token of a decode row (query row q0), kv head h, written
+// into the cache at slot_mapping[q0] by the wave that owns the row's last
+// tile: lanes 0-15 take the k row, lanes 16-31 the v row, 8 elements each.
+// A bf16 cache receives the values; an fp8 / int8 cache the codes and the
+// per-token scale, computed by the store kernel's own helpers (absmax over
+// the row's 16 lanes, quant_scale, quant8), so the bytes are identical.  The
+// rows' cache lines belong to this (slot, head) alone, so the wave's own
+// later loads of the tile see them once the stores have completed.  Slots
+// outside the cache are skipped, as the store kernel skips them.
+template <int KV>
 __device__ __forceinline__ void store_new_token(const DecodeArgs& a, int q0, int h) {
   const int lane = threadIdx.x & 63;
   const int64_t slot = a.slots[q0];
   if (slot < 0 || slot >= a.total_slots || lane >= 32) return;
-  const uint32_t off = lane_off(8u * (uint32_t)(lane & 15) * 2u);
+  const int c = lane & 15;
+  const uint32_t off = lane_off(16u * (uint32_t)c);
   const bool isv = lane >= 16;
   const char* src = (const char*)(isv ? a.vn + (int64_t)q0 * a.vn_ts + (int64_t)h * a.vn_hs
                                       : a.kn + (int64_t)q0 * a.kn_ts + (int64_t)h * a.kn_hs);
-  char* dst = (char*)(isv ? a.vc : a.kc) + (slot * a.Hkv + h) * (int64_t)(kHeadDim * 2);
-  *reinterpret_cast<u32x4*>(dst + off) = *reinterpret_cast<const u32x4*>(src + off);
+  const int64_t row = slot * a.Hkv + h;
+  if constexpr (KV == NVS_DTYPE_BF16) {
+    char* dst = (char*)(isv ? a.vc : a.kc) + row * (int64_t)(kHeadDim * 2);
+    *reinterpret_cast<u32x4*>(dst + off) = *reinterpret_cast<const u32x4*>(src + off);
+  } else {
+    float x[8];
+    load8<NVS_DTYPE_BF16>(src + off, x);
+    constexpr float qmax = (KV == NVS_DTYPE_INT8) ? QuantInt8::kQmax : QuantFp8::kQmax;
+    const float sc = quant_scale(row_absmax(x, kHeadDim / 8), qmax);
+    char* dst = (char*)(isv ? a.vc : a.kc) + row * (int64_t)kHeadDim;
+    *reinterpret_cast<u32x2*>(dst + 8 * c) = quant8<KV>(x, sc);
+    if (c == 0) const_cast<float*>(isv ? a.vs : a.ks)[row] = sc;
+  }
 }
 
 // Zeroes the output of the round's decode rows that see no key (row b by
 // wave b % gridDim.x): no tile covers them, so no wave writes them otherwise.
+template <int KV>
 __device__ __forceinline__ void zero_keyless_rows(const DecodeArgs& a, const ScanRound& rd) {
   const int lane = threadIdx.x & 63;
 #pragma unroll
@@ -471,22 +490,23 @@ __device__ __forceinline__ void zero_keyless_rows(const DecodeArgs& a, const Sca
       }
       // No tile covers this row, so its new token is stored here.
       if (a.kn)
-        for (int h = 0; h < a.Hkv; ++h) store_new_token(a, q0, h);
+        for (int h = 0; h < a.Hkv; ++h) store_new_token<KV>(a, q0, h);
     }
   }
 }
 
 // Total decode tiles of the batch; r0 receives the first scan round, which
 // locate_tile reuses.  Keyless decode rows are zeroed on the way.
+template <int KV>
 __device__ __forceinline__ int decode_tiles(const DecodeArgs& a, const int32_t* __restrict__ cu_q,
                                             const int32_t* __restrict__ cu_k, ScanRound& r0) {
   r0 = load_round(a, cu_q, cu_k, 0);
   int tot = wave_sum_i(lane_tiles(a, r0));
-  zero_keyless_rows(a, r0);
+  zero_keyless_rows<KV>(a, r0);
   for (int c0 = kScanSpan; c0 < a.B; c0 += kScanSpan) {
     const ScanRound rd = load_round(a, cu_q, cu_k, c0);
     tot += wave_sum_i(lane_tiles(a, rd));
-    zero_keyless_rows(a, rd);
+    zero_keyless_rows<KV>(a, rd);
   }
   return tot;
 }
@@ -678,7 +698,7 @@ void paged_decode_kernel(DecodeArgs a, const int32_t* __restrict__ bt, const int
   const int lane = threadIdx.x;
 
   ScanRound r0;
-  const int T = decode_tiles(a, cu_q, cu_k, r0);
+  const int T = decode_tiles<KV>(a, cu_q, cu_k, r0);
   const int Kw = decode_groups(T, G);
   if (w == 0 && lane < 2) a.ws_rec[lane] = lane == 0 ? T : Kw;
   if (k >= Kw) {
@@ -698,6 +718,32 @@ void paged_decode_kernel(DecodeArgs a, const int32_t* __restrict__ bt, const int
     int first;
     locate_tile(a, cu_q, cu_k, s0, r0, n[0], first);
   }
+  // The new tokens of the rows whose last tile lies in this range are
+  // written by this wave (a.kn set), all of them here, before the ring's
+  // state exists, so the walk's registers are free again by the main loop.
+  // The wave's own load of a row's last tile must follow the row's write: a
+  // workgroup-scope release fence (a wait for the wave's own stores, no
+  // cache maintenance) goes before the first loads if a row ends in the
+  // tiles they cover, otherwise just before the load of the first written
+  // row's last tile (fence_tile), so the writes overlap the stream.
+  int fence_tile = INT_MAX;
+  if (a.kn) {
+    Cursor c = n[0];
+    int tile = s0;  // global index of c's tile
+    for (;;) {
+      const int last = tile + (c.n - 1 - c.t);
+      if (last >= s0 + left) break;  // the row ends in a later group's range
+      store_new_token<KV>(a, c.q0, h);
+      fence_tile = min(fence_tile, last);
+      tile = last + 1;
+      if (tile >= s0 + left) break;
+      next_row(a, cu_q, cu_k, c);
+    }
+    if (fence_tile < s0 + D - 1) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+      fence_tile = INT_MAX;
+    }
+  }
   auto advance = [&](Cursor& x) {
     if (++x.t == x.n) {
       next_row(a, cu_q, cu_k, x);
@@ -710,32 +756,6 @@ void paged_decode_kernel(DecodeArgs a, const int32_t* __restrict__ bt, const int
   for (int j = 1; j <= D; ++j) {
     n[j] = n[j - 1];
     if (left > j) advance(n[j]);
-  }
-  // The new tokens of the rows whose last tile lies in this range are
-  // written by this wave (bf16 cache, a.kn set): a row ending inside the
-  // tiles the ring loads first is written before those loads, the others
-  // right after them, so the writes overlap the first loads; a fence then
-  // completes them before any later load is issued.  A wave that wrote
-  // nothing skips the fence (it would wait for the first loads).
-  Cursor sc_c = n[0];
-  int sc_tile = s0;  // global index of sc_c's tile
-  bool sc_more = KV == NVS_DTYPE_BF16 && a.kn != nullptr;
-  auto store_rows = [&](int below) {  // rows whose last tile is < below; true if any
-    bool any = false;
-    while (sc_more) {
-      const int last = sc_tile + (sc_c.n - 1 - sc_c.t);
-      if (last >= s0 + left) { sc_more = false; break; }  // the row ends in a later group's range
-      if (last >= below) break;
-      store_new_token(a, sc_c.q0, h);
-      any = true;
-      sc_tile = last + 1;
-      if (sc_tile >= s0 + left) { sc_more = false; break; }
-      next_row(a, cu_q, cu_k, sc_c);
-    }
-    return any;
-  };
-  if constexpr (KV == NVS_DTYPE_BF16) {
-    if (a.kn && store_rows(s0 + D - 1)) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
   }
 
   bf16x8 qop[4];
@@ -750,14 +770,12 @@ void paged_decode_kernel(DecodeArgs a, const int32_t* __restrict__ bt, const int
   DecodeTile<KV> r[D];
 #pragma unroll
   for (int j = 0; j < D - 1; ++j) decode_load<KV>(r[j], a, lo, tile_block(a, bt, n[j]), n[j].koff, h);
-  if constexpr (KV == NVS_DTYPE_BF16) {
-    if (a.kn && store_rows(s0 + left)) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-  }
   int blk_last = tile_block(a, bt, n[D - 1]);
 
   // Tile i (cursor n[0]) from ring slot cur; the loads of tile i + D - 1 go
   // to slot nxt_t.
   auto step = [&](DecodeTile<KV>& cur, DecodeTile<KV>& nxt_t, int i) {
+    if (s0 + i + D - 1 == fence_tile) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     decode_load<KV>(nxt_t, a, lo, blk_last, n[D - 1].koff, h);
     const int blk_next = tile_block(a, bt, n[D]);
     __builtin_amdgcn_sched_barrier(0);

@@ -369,31 +369,44 @@ class PagedAttention(nn.Module):
 
     def _store_in_decode(self, k, v, context) -> bool:
         """True when the write of a decode batch can ride in the decode
-        kernel: bf16 cache and sources, every row a decode row, and neither
-        write_kv_cache nor store_kv_cache_torch replaced on this layer (the
-        reference's experiments wrap them per instance, and then they must
-        run)."""
+        kernel: bf16 sources, every row a decode row, a bf16 cache (mode
+        "none") or the quantised mode's code cache with fp32 scale caches,
+        and neither write_kv_cache nor store_kv_cache_torch replaced on this
+        layer (the reference's experiments wrap them per instance, and then
+        they must run)."""
         cls = type(self)
+        kc, vc, mode = self.k_cache, self.v_cache, self.kv_cache_quant_mode
+        if kc is None or vc is None:
+            return False
+        if mode == "none":
+            cache_ok = kc.dtype == torch.bfloat16 and vc.dtype == torch.bfloat16
+        elif mode in _QUANT_DTYPE:
+            ks, vs = self.k_scale_cache, self.v_scale_cache
+            cache_ok = (kc.dtype == _QUANT_DTYPE[mode] and vc.dtype == _QUANT_DTYPE[mode]
+                        and ks is not None and vs is not None
+                        and ks.dtype == torch.float32 and vs.dtype == torch.float32
+                        and ks.is_contiguous() and vs.is_contiguous())
+        else:
+            return False
         return (
-            "write_kv_cache" not in self.__dict__ and "store_kv_cache_torch" not in self.__dict__
+            cache_ok
+            and "write_kv_cache" not in self.__dict__ and "store_kv_cache_torch" not in self.__dict__
             and cls.write_kv_cache is PagedAttention.write_kv_cache
             and cls.store_kv_cache_torch is PagedAttention.store_kv_cache_torch
             and self.kv_writer_backend in ("torch", "hip")
             and self.forward_backend in ("flashattn", "hip", "torch")
             and context.block_tables is not None and int(context.max_seqlen_q) == 1
-            and self.kv_cache_quant_mode == "none" and self.attention_compute_dtype == torch.bfloat16
-            and self.k_cache is not None and self.k_cache.dtype == torch.bfloat16
-            and self.v_cache is not None and self.v_cache.dtype == torch.bfloat16
-            and self.k_cache.is_contiguous() and self.v_cache.is_contiguous()
+            and self.attention_compute_dtype == torch.bfloat16
+            and kc.is_contiguous() and vc.is_contiguous()
             and k.dtype == torch.bfloat16 and v.dtype == torch.bfloat16 and k.is_cuda and v.is_cuda
             and k.stride(-1) == 1 and v.stride(-1) == 1
         )
 
     def forward_unified(self, q, k, v, context):
         """Write the step's K/V, then one attention call over the whole batch
-        (attention.py:500-546).  A decode batch over a bf16 cache does both in
-        one call: the decode kernel writes each row's new token before reading
-        its last tile."""
+        (attention.py:500-546).  A decode batch does both in one call: the
+        decode kernel writes each row's new token (bf16 values, or fp8 / int8
+        codes and scales) before reading its last tile."""
         should_profile = self._should_profile()
         if not should_profile and self._store_in_decode(k, v, context):
             return self._attention(q, k, v, context, store_slots=context.slot_mapping)

@@ -398,16 +398,30 @@ def test_determinism_and_batch_split(device, kv):
 
 
 def _cache_bytes(attn):
-    return (attn.k_cache.view(torch.uint8).clone(), attn.v_cache.view(torch.uint8).clone())
+    out = [attn.k_cache.view(torch.uint8).clone(), attn.v_cache.view(torch.uint8).clone()]
+    if attn.k_scale_cache is not None:
+        out += [attn.k_scale_cache.clone(), attn.v_scale_cache.clone()]
+    return out
 
 
-@pytest.mark.parametrize("which", ["decode_small", "decode_8b"])
+_STORE_CASES = {
+    "decode_small": lambda d: W.decode_small(d),
+    "decode_8b": lambda d: W.decode_8b(d),
+    "decode_small/fp8": lambda d: W.decode_small(d, kv="fp8"),
+    "decode_small/int8": lambda d: W.decode_small(d, kv="int8"),
+    "decode_quant/fp8": lambda d: W.decode_quant(d, kv="fp8"),
+    "decode_quant/int8": lambda d: W.decode_quant(d, kv="int8"),
+}
+
+
+@pytest.mark.parametrize("which", list(_STORE_CASES))
 def test_decode_store_in_kernel_equals_store_then_attend(device, which):
-    """forward on a decode batch over a bf16 cache writes the new tokens
-    inside the decode kernel; the cache bytes and the output equal
-    write_kv_cache followed by the attention call, bit for bit."""
+    """forward on a decode batch writes the new tokens inside the decode
+    kernel (bf16 values, or fp8 / int8 codes and per-token scales); the cache
+    bytes, the scales and the output equal write_kv_cache followed by the
+    attention call, bit for bit."""
     say(f"store in the decode kernel: {which}")
-    a, b = W.BUILDERS[which](device), W.BUILDERS[which](device)  # identical seeded workloads
+    a, b = _STORE_CASES[which](device), _STORE_CASES[which](device)  # identical seeded workloads
     assert a.attn._store_in_decode(a.k, a.v, a.context)
     fused = a.attn.forward(a.q, a.k, a.v, a.context)
     b.attn.write_kv_cache(b.k, b.v, b.context.slot_mapping)
@@ -418,13 +432,15 @@ def test_decode_store_in_kernel_equals_store_then_attend(device, which):
         assert torch.equal(x, y), "cache contents differ"
 
 
-def test_decode_store_in_kernel_edge_rows(device):
+@pytest.mark.parametrize("kv", ["bf16", "fp8", "int8"])
+def test_decode_store_in_kernel_edge_rows(device, kv):
     """A decode row with no visible key still has its token written; a
     negative slot is skipped; a wrapped write_kv_cache is still called."""
-    say("store in the decode kernel: keyless row, skipped slot, wrapped writer")
+    say(f"store in the decode kernel ({kv}): keyless row, skipped slot, wrapped writer")
     tabs = _tables([300, 40, 90], 8, 21)
     seqs = [SeqSlice(tabs[0], 299, 1), SeqSlice(tabs[1], 39, 1), SeqSlice(tabs[2], 89, 1)]
-    a, b = _custom(seqs, 8, 2, 8, seed=22), _custom(seqs, 8, 2, 8, seed=22)
+    a, b = _custom(seqs, 8, 2, 8, kv=kv, seed=22), _custom(seqs, 8, 2, 8, kv=kv, seed=22)
+    assert a.attn._store_in_decode(a.k, a.v, a.context)
     for wl in (a, b):
         # Row 1 sees no key (k_len 0); row 2's slot is -1.
         ctx = wl.context
