@@ -29,6 +29,9 @@
 // write back the L2).  The group where a split row starts leaves a record
 // (output row, last group, slot) for the merge, so the merge needs no scan
 // of its own.
+// Given the step's new k / v rows (nvs_paged_attention_store), the wave that
+// owns a decode row's last tile also writes the row's new token into the
+// cache (values, or codes and scales), ahead of its own load of that tile.
 #include <algorithm>
 
 #include "nvs_common.h"
