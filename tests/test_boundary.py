@@ -2,6 +2,7 @@
 KV-pool/config knobs, the step-metadata builder and the guards that fire
 before any launch."""
 import dataclasses
+import ctypes
 import re
 from pathlib import Path
 
@@ -27,6 +28,43 @@ def test_library_exports_every_declared_symbol():
         assert hasattr(lib, name), name
     assert declared == set(_lib.SIGNATURES), declared ^ set(_lib.SIGNATURES)
     assert lib.nvs_version() >= 100
+
+
+def _declared_params(header):
+    """Parameter C types of each nvs_* declaration in the header, in order."""
+    out = {}
+    for m in re.finditer(r"^\s*(?:int|int64_t|const char\*)\s+(nvs_[a-z0-9_]+)\s*\(([^;]*?)\)\s*;", header,
+                         re.M | re.S):
+        body = re.sub(r"/\*.*?\*/", "", m.group(2), flags=re.S).strip()
+        params = [] if body in ("", "void") else [x.strip() for x in body.split(",")]
+        out[m.group(1)] = params
+    return out
+
+
+def _ctype_of(decl):
+    if "*" in decl:
+        return ctypes.c_void_p
+    t = decl.rsplit(" ", 1)[0].replace("const ", "").strip()
+    return {"int": ctypes.c_int, "int64_t": ctypes.c_int64, "float": ctypes.c_float}[t]
+
+
+def test_bindings_match_the_header():
+    """The ctypes argtypes (_lib.SIGNATURES) and the ones INTEGRATION shows a
+    maintainer match every header declaration in count and C type."""
+    header = (ROOT / "include" / "nvs_attention.h").read_text()
+    decls = _declared_params(header)
+    assert set(decls) == set(_lib.SIGNATURES), set(decls) ^ set(_lib.SIGNATURES)
+    for name, params in decls.items():
+        want = [_ctype_of(p) for p in params]
+        got = list(_lib.SIGNATURES[name][1])
+        assert got == want, f"{name}: SIGNATURES {got} vs header {want}"
+    letters = {"P": ctypes.c_void_p, "I": ctypes.c_int, "L": ctypes.c_int64, "F": ctypes.c_float}
+    doc = (ROOT / "INTEGRATION.md").read_text()
+    shown = re.findall(r"lib\.(nvs_[a-z0-9_]+)\.argtypes\s*=\s*\[([^\]]*)\]", doc, re.S)
+    assert shown, "no argtypes in INTEGRATION.md"
+    for name, body in shown:
+        got = [letters[x.strip()] for x in body.split(",") if x.strip()]
+        assert got == list(_lib.SIGNATURES[name][1]), f"INTEGRATION.md argtypes of {name}"
 
 
 def test_context_fields_match_reference():
