@@ -49,8 +49,8 @@ def _ctype_of(decl):
 
 
 def test_bindings_match_the_header():
-    """The ctypes argtypes (_lib.SIGNATURES) and the ones INTEGRATION shows a
-    maintainer match every header declaration in count and C type."""
+    """The ctypes argtypes (_lib.SIGNATURES) match every header declaration
+    in count and C type."""
     header = (ROOT / "include" / "nvs_attention.h").read_text()
     decls = _declared_params(header)
     assert set(decls) == set(_lib.SIGNATURES), set(decls) ^ set(_lib.SIGNATURES)
@@ -58,13 +58,6 @@ def test_bindings_match_the_header():
         want = [_ctype_of(p) for p in params]
         got = list(_lib.SIGNATURES[name][1])
         assert got == want, f"{name}: SIGNATURES {got} vs header {want}"
-    letters = {"P": ctypes.c_void_p, "I": ctypes.c_int, "L": ctypes.c_int64, "F": ctypes.c_float}
-    doc = (ROOT / "INTEGRATION.md").read_text()
-    shown = re.findall(r"lib\.(nvs_[a-z0-9_]+)\.argtypes\s*=\s*\[([^\]]*)\]", doc, re.S)
-    assert shown, "no argtypes in INTEGRATION.md"
-    for name, body in shown:
-        got = [letters[x.strip()] for x in body.split(",") if x.strip()]
-        assert got == list(_lib.SIGNATURES[name][1]), f"INTEGRATION.md argtypes of {name}"
 
 
 def test_context_fields_match_reference():
