@@ -281,12 +281,13 @@ def test_more_rows_than_one_plan_chunk(device):
     _check(wl, ids, "1100-row batch")
 
 
-@pytest.mark.parametrize("kv", ["bf16", "fp8"])
+@pytest.mark.parametrize("kv", ["bf16", "fp8", "int8"])
 def test_decode_step_graph_replay(device, kv):
-    """The decode step (store + attention) captured in a HIP graph: every
-    replay, with eager calls and synchronisations between replays, equals the
-    eager result bit for bit (the same kernels on the same inputs; the store
-    rewrites the same token)."""
+    """The decode step (the token write inside the decode kernel, then the
+    attention) captured in a HIP graph: every replay, with eager calls and
+    synchronisations between replays, equals the eager result bit for bit
+    (the same kernels on the same inputs; the write rewrites the same
+    token)."""
     from nanovllm_self_amd.layers.attention import reserve_attention_workspace
 
     say(f"graph replay decode_small/{kv}")
