@@ -371,10 +371,12 @@ class PagedAttention(nn.Module):
         """True when the write of a decode batch can ride in the decode
         kernel: bf16 sources, every row a decode row, a bf16 cache (mode
         "none") or the quantised mode's code cache with fp32 scale caches,
-        and neither write_kv_cache nor store_kv_cache_torch replaced on this
-        layer (the reference's experiments wrap them per instance, and then
-        they must run)."""
+        and neither write_kv_cache, store_kv_cache_torch nor the attention
+        method forward_unified would call replaced on this layer (the
+        reference's experiments wrap them per instance, and then they must
+        run)."""
         cls = type(self)
+        attn_fn = "prefill_torch" if self.forward_backend == "torch" else "prefill_flashattn"
         kc, vc, mode = self.k_cache, self.v_cache, self.kv_cache_quant_mode
         if kc is None or vc is None:
             return False
@@ -393,6 +395,7 @@ class PagedAttention(nn.Module):
             and "write_kv_cache" not in self.__dict__ and "store_kv_cache_torch" not in self.__dict__
             and cls.write_kv_cache is PagedAttention.write_kv_cache
             and cls.store_kv_cache_torch is PagedAttention.store_kv_cache_torch
+            and attn_fn not in self.__dict__ and getattr(cls, attn_fn) is getattr(PagedAttention, attn_fn)
             and self.kv_writer_backend in ("torch", "hip")
             and self.forward_backend in ("flashattn", "hip", "torch")
             and context.block_tables is not None and int(context.max_seqlen_q) == 1

@@ -463,3 +463,13 @@ def test_decode_store_in_kernel_edge_rows(device, kv):
     again = a.attn.forward(a.q, a.k, a.v, a.context)
     torch.cuda.synchronize()
     assert calls == [1] and torch.equal(again, fused)
+    # A wrapped attention method is called too (the write then runs first).
+    del a.attn.write_kv_cache
+    assert a.attn._store_in_decode(a.k, a.v, a.context)
+    seen = []
+    inner_attn = a.attn.prefill_flashattn
+    a.attn.prefill_flashattn = lambda q, k, v, c: (seen.append(1), inner_attn(q, k, v, c))[1]
+    assert not a.attn._store_in_decode(a.k, a.v, a.context)
+    third = a.attn.forward(a.q, a.k, a.v, a.context)
+    torch.cuda.synchronize()
+    assert seen == [1] and torch.equal(third, fused)
