@@ -236,7 +236,8 @@ int nvs_paged_attention(const void* q, int64_t q_tok_stride,
  * their scales) before it reads the row's last tile (one launch fewer);
  * otherwise the store kernel runs first.  The
  * cache contents and the output equal the two calls made one after the
- * other.
+ * other, for distinct slot_mapping entries (as the engine produces them; a
+ * repeated slot leaves the rows that share it unspecified).
  */
 int nvs_paged_attention_store(const void* q, int64_t q_tok_stride, int64_t q_head_stride,
                               const void* k, const void* v, int src_dtype,
