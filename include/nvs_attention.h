@@ -233,11 +233,20 @@ int nvs_paged_attention(const void* q, int64_t q_tok_stride,
  * attention.py:500-546).  When every row is a decode row (max_seqlen_q ==
  * 1), the sources are BF16 and the rows 16-byte aligned, the decode kernel
  * writes each row's new token itself (BF16 values, or fp8 / int8 codes and
- * their scales) before it reads the row's last tile (one launch fewer);
- * otherwise the store kernel runs first.  The
- * cache contents and the output equal the two calls made one after the
- * other, for distinct slot_mapping entries (as the engine produces them; a
- * repeated slot leaves the rows that share it unspecified).
+ * their scales); otherwise the store kernel runs first.  In the decode
+ * kernel, the wave that reads a row's last tile writes the row's token just
+ * before that read when slot_mapping[row] is the row's own last position
+ * (block_tables[row][(k_len-1) / block_size] * block_size + (k_len-1) %
+ * block_size, the slot the engine forms for a decode row); any other slot
+ * >= 0 (a keyless row, a missing block, a position in another row's keys or
+ * an earlier tile of its own) is detected on the device and written by every
+ * wave of its kv head before that wave's first load.
+ * Precondition: slot_mapping entries are distinct (a repeated slot leaves
+ * the rows that share it unspecified), and no row reads another row's
+ * own-last-position slot through a shared block (a sequence appends only
+ * into its own last block, as the engine's block manager guarantees).
+ * Under it, the cache contents and the output equal nvs_store_kvcache
+ * followed by nvs_paged_attention, bit for bit.
  */
 int nvs_paged_attention_store(const void* q, int64_t q_tok_stride, int64_t q_head_stride,
                               const void* k, const void* v, int src_dtype,

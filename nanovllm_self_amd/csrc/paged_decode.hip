@@ -31,7 +31,11 @@
 // of its own.
 // Given the step's new k / v rows (nvs_paged_attention_store), the wave that
 // owns a decode row's last tile also writes the row's new token into the
-// cache (values, or codes and scales), ahead of its own load of that tile.
+// cache (values, or codes and scales), ahead of its own load of that tile,
+// when the row's slot is its own last position k_len - 1 under its block
+// table (the slot the engine gives a decode row).  Every other slot is
+// checked for on the device and written, before any load, by every wave that
+// reads the cache (see write_nonconforming).
 #include <algorithm>
 
 #include "nvs_common.h"
@@ -440,18 +444,16 @@ __device__ __forceinline__ int wave_incl_scan(int v) {
 }
 
 // The step's new token of a decode row (query row q0), kv head h, written
-// into the cache at slot_mapping[q0] by the wave that owns the row's last
-// tile: lanes 0-15 take the k row, lanes 16-31 the v row, 8 elements each.
-// A bf16 cache receives the values; an fp8 / int8 cache the codes and the
-// per-token scale, computed by the store kernel's own helpers (absmax over
-// the row's 16 lanes, quant_scale, quant8), so the bytes are identical.  The
-// rows' cache lines belong to this (slot, head) alone, so the wave's own
-// later loads of the tile see them once the stores have completed.  Slots
-// outside the cache are skipped, as the store kernel skips them.
+// into the cache at `slot` (slot_mapping[q0]): lanes 0-15 take the k row,
+// lanes 16-31 the v row, 8 elements each.  A bf16 cache receives the
+// values; an fp8 / int8 cache the codes and the per-token scale, computed by
+// the store kernel's own helpers (absmax over the row's 16 lanes,
+// quant_scale, quant8), so the bytes are identical whichever wave writes
+// them.  Slots outside the cache are skipped, as the store kernel skips
+// them.
 template <int KV>
-__device__ __forceinline__ void store_new_token(const DecodeArgs& a, int q0, int h) {
+__device__ __forceinline__ void store_new_token(const DecodeArgs& a, int q0, int64_t slot, int h) {
   const int lane = threadIdx.x & 63;
-  const int64_t slot = a.slots[q0];
   if (slot < 0 || slot >= a.total_slots || lane >= 32) return;
   const int c = lane & 15;
   const uint32_t off = lane_off(16u * (uint32_t)c);
@@ -491,11 +493,94 @@ __device__ __forceinline__ void zero_keyless_rows(const DecodeArgs& a, const Sca
         const int hq = x / (kHeadDim / 8), d = 8 * (x % (kHeadDim / 8));
         *reinterpret_cast<u32x4*>(a.out + (int64_t)q0 * a.out_ts + (int64_t)hq * a.out_hs + d) = u32x4{0, 0, 0, 0};
       }
-      // No tile covers this row, so its new token is stored here.
-      if (a.kn)
-        for (int h = 0; h < a.Hkv; ++h) store_new_token<KV>(a, q0, h);
     }
   }
+}
+
+// ---------------------------------------------------------------------------
+// Where the step's new tokens may be written from.  The owner of a decode
+// row's last tile writes the row's token ahead of its own load of that tile
+// when the slot is the row's own last position (slot == block_table[row][
+// (k_len - 1) / bs] * bs + (k_len - 1) % bs, the slot the engine forms for a
+// decode row): no other wave reads that position as long as no other row of
+// the batch reads the row's last block at that offset (a sequence appends
+// only into its own last block).  Any other valid slot (a keyless row, a
+// missing block, a slot in another row's keys or in an earlier tile of its
+// own row) could be read by any wave of the kv head, so every such wave
+// writes it before its first load: the bytes are the same from every wave,
+// so each wave reads the new token (its own write, or an identical one), as
+// after the reference's write-then-read.  Negative slots and slots outside
+// the cache are skipped, as the store kernel skips them.
+// ---------------------------------------------------------------------------
+struct SlotCheck {
+  int slot[kScanRows];  // slot_mapping of the lane's rows (-1 for non-decode rows)
+  int blk[kScanRows];   // block-table entry of their last position (-1: none)
+  int off[kScanRows];   // that position's offset in its block (-1: keyless row)
+};
+
+// Loads of a scan round's slots and last-position block ids (vector loads,
+// issued early; the values are used after the tile search).
+__device__ __forceinline__ SlotCheck issue_slot_check(const DecodeArgs& a, const int32_t* __restrict__ bt,
+                                                      const ScanRound& rd) {
+  SlotCheck c;
+  const int b0 = rd.c0 + kScanRows * (int)threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < kScanRows; ++i) {
+    const int b = b0 + i;
+    const bool dec = b < a.B && rd.q[i + 1] - rd.q[i] == 1 && rd.q[i] >= 0 && (int64_t)rd.q[i + 1] <= a.T;
+    const int K = rd.k[i + 1] - rd.k[i];
+    const int lb = K > 0 ? (K - 1) / a.bs : 0;
+    c.slot[i] = -1;
+    c.blk[i] = -1;
+    c.off[i] = K > 0 ? K - 1 - lb * a.bs : -1;
+    if (dec) c.slot[i] = a.slots[rd.q[i]];
+    if (dec && K > 0 && lb < a.bt_stride) c.blk[i] = bt[(int64_t)b * a.bt_stride + lb];
+  }
+  return c;
+}
+
+// Whether a decode row's token may be left to the owner of its last tile:
+// its slot is skipped, or it is the row's last position, offset `off`
+// (-1: the row has no key) in block `blk` (-1: none).
+__device__ __forceinline__ bool owner_writes(const DecodeArgs& a, int64_t slot, int blk, int off) {
+  if (slot < 0 || slot >= a.total_slots) return true;  // skipped by every writer
+  if (off < 0 || blk < 0 || blk >= a.NB) return false;
+  return slot == (int64_t)blk * a.bs + off;
+}
+
+// Every wave of kv head h writes the round's rows that no owner writes
+// (ballot over the lanes' rows); true if there was one.
+template <int KV>
+__device__ __forceinline__ bool write_nonconforming(const DecodeArgs& a, const ScanRound& rd,
+                                                    const SlotCheck& c, int h) {
+  bool any = false;
+#pragma unroll
+  for (int i = 0; i < kScanRows; ++i) {
+    const bool bad = !owner_writes(a, c.slot[i], c.blk[i], c.off[i]);
+    uint64_t z = __ballot(bad);
+    any |= z != 0;
+    while (z) {
+      const int li = __builtin_ctzll(z);
+      z &= z - 1;
+      store_new_token<KV>(a, __builtin_amdgcn_readlane(rd.q[i], li), __builtin_amdgcn_readlane(c.slot[i], li), h);
+    }
+  }
+  return any;
+}
+
+// The all-waves writes of the whole batch: round 0 from the checks issued at
+// the start, later rounds (more than 256 rows) loaded here.
+template <int KV>
+__device__ __forceinline__ bool write_all_nonconforming(const DecodeArgs& a, const int32_t* __restrict__ bt,
+                                                        const int32_t* __restrict__ cu_q,
+                                                        const int32_t* __restrict__ cu_k, const ScanRound& r0,
+                                                        const SlotCheck& c0, int h) {
+  bool any = write_nonconforming<KV>(a, r0, c0, h);
+  for (int s = kScanSpan; s < a.B; s += kScanSpan) {
+    const ScanRound rd = load_round(a, cu_q, cu_k, s);
+    any |= write_nonconforming<KV>(a, rd, issue_slot_check(a, bt, rd), h);
+  }
+  return any;
 }
 
 // Total decode tiles of the batch; r0 receives the first scan round, which
@@ -704,8 +789,14 @@ void paged_decode_kernel(DecodeArgs a, const int32_t* __restrict__ bt, const int
   const int T = decode_tiles<KV>(a, cu_q, cu_k, r0);
   const int Kw = decode_groups(T, G);
   if (w == 0 && lane < 2) a.ws_rec[lane] = lane == 0 ? T : Kw;
+  // The slot checks of the first 256 rows, waited for after the tile search.
+  SlotCheck chk0;
+  if (a.kn) chk0 = issue_slot_check(a, bt, r0);
   if (k >= Kw) {
     if (lane == 0) a.ws_rec[4 + 4 * w + 3] = 0;
+    // With no tile at all no wave reads the cache; group 0 still writes the
+    // rows no owner writes.
+    if (a.kn && k == 0) write_all_nonconforming<KV>(a, bt, cu_q, cu_k, r0, chk0, h);
     return;
   }
   const int s0 = group_start(T, Kw, k);
@@ -721,14 +812,16 @@ void paged_decode_kernel(DecodeArgs a, const int32_t* __restrict__ bt, const int
     int first;
     locate_tile(a, cu_q, cu_k, s0, r0, n[0], first);
   }
-  // The new tokens of the rows whose last tile lies in this range are
-  // written by this wave (a.kn set), all of them here, before the ring's
-  // state exists, so the walk's registers are free again by the main loop.
-  // The wave's own load of a row's last tile must follow the row's write: a
-  // workgroup-scope release fence (a wait for the wave's own stores, no
-  // cache maintenance) goes before the first loads if a row ends in the
-  // tiles they cover, otherwise just before the load of the first written
-  // row's last tile (fence_tile), so the writes overlap the stream.
+  // The new tokens of the rows whose last tile lies in this range and whose
+  // slot is their own last position are written by this wave (a.kn set),
+  // all of them here, before the ring's state exists, so the walk's
+  // registers are free again by the main loop; then the rows no owner
+  // writes, by every wave.  The wave's own load of a row's last tile must
+  // follow the row's write: a workgroup-scope release fence (a wait for the
+  // wave's own stores, no cache maintenance) goes before the first loads if
+  // a row ends in the tiles they cover or the wave wrote a row no owner
+  // writes, otherwise just before the load of the first written row's last
+  // tile (fence_tile), so the writes overlap the stream.
   int fence_tile = INT_MAX;
   if (a.kn) {
     Cursor c = n[0];
@@ -736,12 +829,18 @@ void paged_decode_kernel(DecodeArgs a, const int32_t* __restrict__ bt, const int
     for (;;) {
       const int last = tile + (c.n - 1 - c.t);
       if (last >= s0 + left) break;  // the row ends in a later group's range
-      store_new_token<KV>(a, c.q0, h);
-      fence_tile = min(fence_tile, last);
+      const int64_t slot = a.slots[c.q0];
+      const int lb = (c.K - 1) / a.bs;  // c.K >= 1: the row has tiles
+      const int blk = lb < a.bt_stride ? bt[(int64_t)c.b * a.bt_stride + lb] : -1;
+      if (owner_writes(a, slot, blk, c.K - 1 - lb * a.bs)) {
+        store_new_token<KV>(a, c.q0, slot, h);
+        fence_tile = min(fence_tile, last);
+      }
       tile = last + 1;
       if (tile >= s0 + left) break;
       next_row(a, cu_q, cu_k, c);
     }
+    if (write_all_nonconforming<KV>(a, bt, cu_q, cu_k, r0, chk0, h)) fence_tile = s0;
     if (fence_tile < s0 + D - 1) {
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
       fence_tile = INT_MAX;

@@ -16,6 +16,7 @@ by both.
 from __future__ import annotations
 
 import math
+import os
 from time import perf_counter
 
 import torch
@@ -143,6 +144,10 @@ class PagedAttention(nn.Module):
 
         self.kv_writer_backend = "torch"
         self.forward_backend = "flashattn"
+        # Debug check of the one-call decode write's precondition (no row of
+        # the batch reads another row's new-token position); it synchronises,
+        # so it is off by default and never runs during graph capture.
+        self.verify_decode_slots = os.environ.get("NVS_VERIFY_DECODE_SLOTS", "0") == "1"
 
     def _should_profile(self):
         return self.enable_profile and (not self.in_cuda_graph_capture)
@@ -405,13 +410,44 @@ class PagedAttention(nn.Module):
             and k.stride(-1) == 1 and v.stride(-1) == 1
         )
 
+    def _decode_slots_private(self, context) -> bool:
+        """Host check (one synchronisation) of what the one-call decode write
+        relies on beyond what the kernel checks itself: no row of the batch
+        reads the position of a row's new token except that row at its own
+        last position, i.e. no (row, logical block j) with block_tables[row,
+        j] == slot // bs and j * bs + slot % bs < k_len, other than the
+        writer's own last block.  The engine's block manager guarantees it
+        (a sequence appends only into its own last block); a batch that
+        breaks it takes the store kernel first."""
+        bt = context.block_tables
+        slots = context.slot_mapping.to(torch.int64)
+        cu_k = context.cu_seqlens_k.to(torch.int64)
+        klen = cu_k[1:] - cu_k[:-1]
+        bs = self.k_cache.shape[1]
+        B, W = bt.shape
+        if B == 0 or slots.numel() == 0:
+            return True
+        rows = torch.arange(B, device=bt.device)
+        sblk, soff = slots // bs, slots % bs                        # [T]
+        own = torch.clamp(klen - 1, min=0) // bs                    # [B] each row's last logical block
+        tok = torch.arange(slots.numel(), device=bt.device)
+        cu_q = context.cu_seqlens_q.to(torch.int64)
+        writer = torch.searchsorted(cu_q[1:], tok, right=True).clamp(max=B - 1)  # row of token t
+        j = torch.arange(W, device=bt.device)
+        hit = (bt.to(torch.int64)[None, :, :] == sblk[:, None, None]) & (slots >= 0)[:, None, None]
+        hit &= (j[None, None, :] * bs + soff[:, None, None]) < klen[None, :, None]
+        hit &= ~((rows[None, :, None] == writer[:, None, None]) & (j[None, None, :] == own[writer][:, None, None]))
+        return not bool(hit.any().item())
+
     def forward_unified(self, q, k, v, context):
         """Write the step's K/V, then one attention call over the whole batch
         (attention.py:500-546).  A decode batch does both in one call: the
         decode kernel writes each row's new token (bf16 values, or fp8 / int8
         codes and scales) before reading its last tile."""
         should_profile = self._should_profile()
-        if not should_profile and self._store_in_decode(k, v, context):
+        if not should_profile and self._store_in_decode(k, v, context) and (
+                not self.verify_decode_slots or self.in_cuda_graph_capture
+                or self._decode_slots_private(context)):
             return self._attention(q, k, v, context, store_slots=context.slot_mapping)
         if should_profile:
             torch.cuda.synchronize()

@@ -11,10 +11,17 @@ from oracle import kv_oracle as KO
 
 BF16_MAX_ABS, BF16_MEAN_ABS = 2e-2, 2e-3  # bf16 KV vs the fp32 oracle
 QUANT_MAX_ABS = 5e-2                       # int8 / fp8 KV vs the fp32 oracle
+QUANT_MEAN_ABS = 5e-3                      # int8 / fp8 KV mean (a bar of this suite's own)
 # The reference returns bf16 (.to(self.dtype), attention.py:498), so every
 # output, its own included, carries up to half a bf16 ulp (<= 2^-8 |x|) of
 # rounding on top of the absolute bound.
 BF16_HALF_ULP_REL = 2.0 ** -8
+# The stated bars are raw max-abs bounds.  A bf16 output of magnitude >= 4
+# carries up to 2^-7 (>= 8: 2^-6 ... ) of rounding alone, so no bf16 output,
+# the reference's included, can meet a raw 2e-2 there; the raw bound is
+# checked on every element below RAW_BOUND_BELOW, the rounding-adjusted bound
+# on every element.
+RAW_BOUND_BELOW = 4.0
 
 
 def say(*args):
@@ -89,10 +96,37 @@ def compare(got: np.ndarray, ref: np.ndarray, quant: bool, what: str):
     err = np.abs(got.astype(np.float64) - ref.astype(np.float64))
     mx, mean = float(err.max()), float(err.mean())
     # error beyond the output's own bf16 rounding allowance
-    excess = float((err - BF16_HALF_ULP_REL * np.abs(ref.astype(np.float64))).max())
-    say(f"{what}: max-abs {mx:.3e} mean-abs {mean:.3e} max-abs beyond bf16 rounding {excess:.3e}")
+    mag = np.abs(ref.astype(np.float64))
+    excess = float((err - BF16_HALF_ULP_REL * mag).max())
+    small = mag < RAW_BOUND_BELOW
+    raw = float(err[small].max()) if small.any() else 0.0
+    say(f"{what}: max-abs {mx:.3e} (|ref| < {RAW_BOUND_BELOW:g}: {raw:.3e}, max |ref| {float(mag.max()):.2f}) "
+        f"mean-abs {mean:.3e} max-abs beyond bf16 rounding {excess:.3e}")
     atol = QUANT_MAX_ABS if quant else BF16_MAX_ABS
+    mtol = QUANT_MEAN_ABS if quant else BF16_MEAN_ABS
+    assert raw <= atol, f"{what}: max-abs {raw:.3e} > {atol} where |ref| < {RAW_BOUND_BELOW:g}"
     assert excess <= atol, f"{what}: max-abs beyond bf16 output rounding {excess:.3e} > {atol}"
-    if not quant:
-        assert mean <= BF16_MEAN_ABS, f"{what}: mean-abs {mean:.3e} > {BF16_MEAN_ABS}"
+    assert mean <= mtol, f"{what}: mean-abs {mean:.3e} > {mtol}"
     return mx, mean
+
+
+def oracle_seq_rows(wl, i, r0, r1):
+    """fp32 oracle for query rows r0 .. r1-1 of sequence i of a paged workload.
+
+    Under the bottom-right causal mask, row r of a sequence with P cached and
+    L new tokens sees keys 0 .. P + r.  A contiguous row block [r0, r1) is
+    therefore itself a sequence with q_len = r1 - r0 new tokens over
+    k_len = P + r1 keys (its row j sees keys up to j + k_len - q_len =
+    P + r0 + j), so long sequences are checked block by block at the cost of
+    the block alone.  Returns (oracle rows, their indices in the batch)."""
+    s = wl.seqs[i]
+    bs = wl.block_size
+    klen = s.num_cached_tokens + r1
+    need = (klen + bs - 1) // bs
+    kv, vv = cache_blocks_f32(wl.attn, np.asarray(s.block_table[:need]))
+    q0 = int(wl.context.cu_seqlens_q[i].item())
+    q = torch.from_numpy(bf16_to_np(wl.q[q0 + r0:q0 + r1]))
+    bt = np.arange(need, dtype=np.int64)[None]
+    ref = AO.paged_attention(q, kv, vv, bt, [0, r1 - r0], [0, klen], [klen], wl.num_heads,
+                             wl.num_kv_heads, wl.head_dim)
+    return ref.numpy(), list(range(q0 + r0, q0 + r1))

@@ -473,3 +473,110 @@ def test_decode_store_in_kernel_edge_rows(device, kv):
     third = a.attn.forward(a.q, a.k, a.v, a.context)
     torch.cuda.synchronize()
     assert seen == [1] and torch.equal(third, fused)
+
+
+def _slot_of(wl, row, pos):
+    s = wl.seqs[row]
+    bs = wl.block_size
+    return s.block_table[pos // bs] * bs + pos % bs
+
+
+def _fused_vs_plain(a, b):
+    """forward() on `a` (one call, decode kernel writes) against
+    write_kv_cache + the attention call on `b` (same seeded workload and
+    context edits): output and every cache byte equal."""
+    fused = a.attn.forward(a.q, a.k, a.v, a.context)
+    b.attn.write_kv_cache(b.k, b.v, b.context.slot_mapping)
+    plain = b.attn.prefill_flashattn(b.q, b.k, b.v, b.context)
+    torch.cuda.synchronize()
+    assert torch.equal(fused, plain), "output differs from store-then-attend"
+    for x, y in zip(_cache_bytes(a.attn), _cache_bytes(b.attn)):
+        assert torch.equal(x, y), "cache contents differ"
+    return fused
+
+
+_SLOT_CASES = ["other_row", "earlier_tile", "keyless_in_range", "missing_last_block"]
+
+
+@pytest.mark.parametrize("kv", ["bf16", "fp8", "int8"])
+@pytest.mark.parametrize("case", _SLOT_CASES)
+def test_decode_store_slot_not_own_position(device, kv, case):
+    """A decode row whose slot is not its own last position (a distinct slot
+    inside another row's keys, in an earlier tile of its own row, the slot
+    of a keyless row inside another row's keys, a row whose last block is
+    missing) is found on the device and written by every wave of its kv head
+    before any load: forward() still equals write_kv_cache followed by the
+    attention, bit for bit (the reference's write-then-read,
+    attention.py:516, 539)."""
+    say(f"store in the decode kernel, slot not the row's own position: {case} {kv}")
+    a, b = W.decode_small(device, kv=kv), W.decode_small(device, kv=kv)
+    for wl in (a, b):
+        ctx = wl.context
+        ctx.slot_mapping = ctx.slot_mapping.clone()
+        if case == "other_row":
+            # row 0's token lands at position 10 of row 1 (read by row 1's waves)
+            ctx.slot_mapping[0] = _slot_of(wl, 1, 10)
+        elif case == "earlier_tile":
+            # row 2's token lands at position 3 of its own keys (its first tile)
+            ctx.slot_mapping[2] = _slot_of(wl, 2, 3)
+        elif case == "keyless_in_range":
+            # row 3 sees no key; its slot is position 40 of row 4
+            lens = (ctx.cu_seqlens_k[1:] - ctx.cu_seqlens_k[:-1]).clone()
+            lens[3] = 0
+            ctx.cu_seqlens_k = torch.cat([torch.zeros(1, dtype=torch.int32, device=device),
+                                          torch.cumsum(lens, 0).to(torch.int32)])
+            ctx.context_lens = lens.to(torch.int32)
+            ctx.slot_mapping[3] = _slot_of(wl, 4, 40)
+        else:
+            # row 5's last block entry is -1: its slot (position k_len - 1 of
+            # the original table) is read by nobody, but is still written
+            n = wl.seqs[5].num_cached_tokens
+            ctx.block_tables = ctx.block_tables.clone()
+            ctx.block_tables[5, n // wl.block_size] = -1
+    assert a.attn._store_in_decode(a.k, a.v, a.context)
+    _fused_vs_plain(a, b)
+
+
+@pytest.mark.parametrize("kv", ["bf16", "fp8"])
+def test_decode_store_slot_cases_at_size(device, kv):
+    """The same on the 256-row quantised-decode shape (many groups split every
+    row): three rows' slots moved into other rows' keys."""
+    say(f"store in the decode kernel, moved slots at size ({kv})")
+    a, b = W.decode_quant(device, kv=kv), W.decode_quant(device, kv=kv)
+    for wl in (a, b):
+        ctx = wl.context
+        ctx.slot_mapping = ctx.slot_mapping.clone()
+        ctx.slot_mapping[0] = _slot_of(wl, 200, 700)
+        ctx.slot_mapping[17] = _slot_of(wl, 17, 100)
+        ctx.slot_mapping[255] = _slot_of(wl, 3, 1000)
+    _fused_vs_plain(a, b)
+
+
+def test_decode_store_shared_block_takes_store_path(device, monkeypatch):
+    """A row's own last position read by another row through a shared block is
+    outside what the decode kernel checks; with verify_decode_slots the layer
+    finds it on the host and runs the store kernel first, so the result equals
+    store-then-attend; the engine's batches pass the check."""
+    say("store in the decode kernel: shared last block, verify_decode_slots")
+    from nanovllm_self_amd import _lib
+    a, b = W.decode_small(device), W.decode_small(device)
+    assert a.attn._decode_slots_private(a.context)
+    bs = a.block_size
+    n0 = a.seqs[0].num_cached_tokens  # row 0's new token sits at position n0
+    lens = (a.context.cu_seqlens_k[1:] - a.context.cu_seqlens_k[:-1]).tolist()
+    r2 = next(r for r in range(1, a.num_seqs) if lens[r] > n0 % bs)
+    for wl in (a, b):
+        ctx = wl.context
+        ctx.block_tables = ctx.block_tables.clone()
+        # row r2's first block becomes row 0's last block: r2 reads row 0's
+        # new-token position
+        ctx.block_tables[r2, 0] = ctx.block_tables[0, n0 // bs]
+    a.attn.verify_decode_slots = True
+    assert a.attn._store_in_decode(a.k, a.v, a.context)
+    assert not a.attn._decode_slots_private(a.context)
+    lib = _lib.load()
+    calls = []
+    inner = lib.nvs_store_kvcache
+    monkeypatch.setattr(lib, "nvs_store_kvcache", lambda *args: (calls.append(1), inner(*args))[1])
+    _fused_vs_plain(a, b)
+    assert len(calls) == 2, "the layer must run the store kernel (and b's write_kv_cache one more)"
