@@ -263,6 +263,36 @@ int nvs_paged_attention_store(const void* q, int64_t q_tok_stride, int64_t q_hea
                               void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * Allocation-free variant of nvs_paged_attention_store, with no counterpart
+ * in the reference: for callers that cannot allocate device memory or pass a
+ * workspace (code under HIP-graph capture, tight serving loops, hosts that
+ * forbid hipMalloc).  Same arguments, semantics and kernels as
+ * nvs_paged_attention_store without workspace / workspace_bytes: the
+ * workspace is the library's static per-device scratch of
+ * NVS_NOALLOC_SCRATCH_BYTES (32 MiB on every GPU the library is loaded on,
+ * held until the process ends), looked up on the first call with the device
+ * current; the stream must belong to the current device.  A batch whose
+ * nvs_attention_workspace_bytes(...) exceeds the scratch is refused with
+ * NVS_ERR_WORKSPACE before anything is launched.  The call allocates
+ * nothing.  Every call on one GPU shares that GPU's scratch: calls that
+ * overlap on one GPU (different streams or threads) race; calls ordered on
+ * one stream do not.
+ */
+#define NVS_NOALLOC_SCRATCH_BYTES (32ll << 20)
+int nvs_paged_attention_store_noalloc(const void* q, int64_t q_tok_stride, int64_t q_head_stride,
+                                      const void* k, const void* v, int src_dtype,
+                                      int64_t k_tok_stride, int64_t k_head_stride,
+                                      int64_t v_tok_stride, int64_t v_head_stride,
+                                      const int32_t* slot_mapping, void* k_cache, void* v_cache,
+                                      int cache_dtype, float* k_scale, float* v_scale,
+                                      const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                                      const int32_t* block_tables, int64_t bt_stride, int num_seqs,
+                                      int64_t num_tokens, int max_seqlen_q, int max_seqlen_k,
+                                      int num_heads, int num_kv_heads, int head_dim, int block_size,
+                                      int64_t num_blocks, float softmax_scale, void* out,
+                                      int64_t out_tok_stride, int64_t out_head_stride, void* stream);
+
+/*
  * Causal varlen attention over the step's own (not cached) K/V: the
  * block_tables-is-None call of prefill_flashattn (reference
  * attention.py:338-354, flash_attn_varlen_func without block_table) and the

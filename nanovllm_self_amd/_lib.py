@@ -73,6 +73,19 @@ SIGNATURES = {
             _P, _L, _P,  # workspace, bytes, stream
         ],
     ),
+    "nvs_paged_attention_store_noalloc": (
+        _I,
+        [
+            _P, _L, _L,  # q
+            _P, _P, _I, _L, _L, _L, _L, _P,  # k, v, src dtype, strides, slot_mapping
+            _P, _P, _I, _P, _P,  # caches, dtype, scales
+            _P, _P, _P, _L,  # cu_q, cu_k, block_tables, bt_stride
+            _I, _L, _I, _I,  # num_seqs, num_tokens, max_q, max_k
+            _I, _I, _I, _I, _L,  # heads, kv heads, head_dim, block_size, num_blocks
+            _F, _P, _L, _L,  # scale, out
+            _P,  # stream
+        ],
+    ),
     "nvs_qk_norm_rope_store": (
         _I,
         [
