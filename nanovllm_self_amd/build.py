@@ -55,8 +55,16 @@ def _compile(src: Path) -> Path:
     return obj
 
 
+def generate() -> None:
+    """Regenerate the prefill kernel's tile loop (csrc/prefill_mx_asm.inc)."""
+    res = subprocess.run([sys.executable, str(CSRC / "gen_prefill_mx.py")], capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"gen_prefill_mx.py failed:\n{res.stderr}")
+
+
 def build(verbose: bool = True) -> Path:
     """Compile every HIP source and link the shared library; returns its path."""
+    generate()
     BUILD_DIR.mkdir(exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))
     if not sources:

@@ -62,9 +62,16 @@ int64_t attention_workspace_bytes(int num_seqs, int max_seqlen_q, int max_seqlen
   return align256(plan_bytes(num_seqs, ntq)) + decode_workspace_bytes(waves, group);
 }
 
+// The plan's tile of query positions is the kernel's work-item height; the
+// classic kernel's tile is never larger than the MFMA tile-loop kernel's,
+// so the workspace sized for it holds either plan.
 static Plan make_plan(void* ws, const AttnParams& P) {
-  const int pbm = prefill_pbm(P.Hq, P.Hkv);
+  const int pbm = prefill_mx_serves(P) ? prefill_mx_positions(P.Hq / P.Hkv) : prefill_pbm(P.Hq, P.Hkv);
   return plan_at(ws, prefill_tiles(P.max_seqlen_q, pbm), pbm);
+}
+
+static int launch_prefill_any(const AttnParams& P, const Plan& plan, hipStream_t s) {
+  return prefill_mx_serves(P) ? launch_prefill_mx(P, plan, s) : launch_prefill(P, plan, s);
 }
 
 int decode_launch_waves(int max_waves, int Hkv) {
@@ -145,7 +152,7 @@ static int paged_attention_impl(AttnParams& P, const void* q, int64_t q_tok_stri
   if (rc != NVS_OK || max_seqlen_q == 1) return rc;  // no prefill rows: no plan
   rc = launch_plan(P, plan, /*paged=*/true, s);
   if (rc != NVS_OK) return rc;
-  return launch_prefill(P, plan, s);
+  return launch_prefill_any(P, plan, s);
 }
 
 extern "C" int nvs_paged_attention(const void* q, int64_t q_tok_stride, int64_t q_head_stride,
@@ -245,5 +252,5 @@ extern "C" int nvs_varlen_attention(const void* q, int64_t q_tok_stride, int64_t
   const Plan plan = make_plan(workspace, P);
   rc = launch_plan(P, plan, /*paged=*/false, s);
   if (rc != NVS_OK) return rc;
-  return launch_prefill(P, plan, s);
+  return launch_prefill_any(P, plan, s);
 }

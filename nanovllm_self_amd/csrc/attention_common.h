@@ -190,5 +190,11 @@ int decode_launch_waves(int max_waves, int Hkv);
 int launch_plan(const AttnParams& P, const Plan& plan, bool paged, hipStream_t stream);
 int launch_decode(const AttnParams& P, int max_waves, int waves, void* partials, hipStream_t stream);
 int launch_prefill(const AttnParams& P, const Plan& plan, hipStream_t stream);
+// The MFMA tile-loop prefill kernel (paged_prefill_mx.hip): whether it serves
+// a call, its query positions per work item for a group of g query heads,
+// and its launch.
+bool prefill_mx_serves(const AttnParams& P);
+int prefill_mx_positions(int g);
+int launch_prefill_mx(const AttnParams& P, const Plan& plan, hipStream_t stream);
 
 }  // namespace nvs

@@ -1,0 +1,641 @@
+#!/usr/bin/env python3
+"""Generator of the hand-scheduled tile loop of the MFMA prefill kernel
+(paged_prefill_mx.hip) for gfx950.
+
+Writes prefill_mx_asm.inc next to this file: two string-literal macros
+(NVS_PREFILL_MX_ASM_PAGED, NVS_PREFILL_MX_ASM_LOCAL), each the body of one
+inline-asm statement that runs a work item's whole tile loop.  Run it after
+editing this file:  python nanovllm_self_amd/csrc/gen_prefill_mx.py
+
+Per wave: 64 query rows as two 32-row q-blocks (qb), one 64-key tile per
+iteration, v_mfma_f32_32x32x16_bf16 throughout:
+  S^T[kb][qb] (32 keys x 32 q)  = K . Q^T   16 d-steps x ... = 32 MFMAs
+  O^T[n][qb]  (32 d x 32 q)    += V^T . P^T                   32 MFMAs
+Iteration j: segment A runs PV of tile j-1 beside the row max / running-max
+update of S_j and the first exponentials; segment B runs QK of tile j+1
+beside the rest of S_j's exponentials, the bf16 packing of P_j and the row
+sums.  K/V operands are read from LDS into an AGPR ring four operands ahead
+of their MFMAs; the next tiles are copied HBM -> LDS with buffer loads that
+write LDS directly (out-of-range rows read as zero).
+
+Register map (fixed; the C++ side binds inputs and outputs to it):
+  v[0:127]    S_j / S_{j+1}: S[par][kb][qb] = v[64 par + 16 (2 kb + qb) ..]
+  v[128:191]  P_j / P_{j-1}: P[par][qb][m] = v[128 + 32 par + 16 qb + 4 m ..]
+  v[192:199]  K operand LDS addresses, one per d-step st (K buffer 0, kb 0)
+  v[200:207]  V operand LDS addresses, per (d-block n, key half e)
+  v[208:211]  K DMA lane offsets, v[212:215] V DMA lane offsets
+  v216-217 m_run, v218-219 l_run (out), v220-221 mask limit (in/out)
+  v222 -inf, v223 bf16 (1, 1), v224-231 softmax temporaries,
+  v232-239 exponential temporaries, v240 block id
+  a[0:63]     Q^T operands: Q[qb][st] = a[32 qb + 4 st ..]   (in)
+  a[64:191]   O^T accumulators: O[n][qb] = a[64 + 16 (2 n + qb) ..] (out)
+  a[192:223]  V operand ring (8 slots), a[224:255] K operand ring (8 slots)
+  s[40:52]    scalar inputs, s[64:101] loop state
+"""
+from __future__ import annotations
+
+import os
+import sys
+
+MF = "v_mfma_f32_32x32x16_bf16"
+
+# ----------------------------------------------------------- register map
+def S(par, kb, qb):
+    b = 64 * par + 16 * (2 * kb + qb)
+    return f"v[{b}:{b + 15}]"
+
+
+def Sr(par, kb, qb, v):
+    return f"v{64 * par + 16 * (2 * kb + qb) + v}"
+
+
+def P(par, qb, m):
+    b = 128 + 32 * par + 16 * qb + 4 * m
+    return f"v[{b}:{b + 3}]"
+
+
+def Pr(par, qb, m, e):
+    return f"v{128 + 32 * par + 16 * qb + 4 * m + e}"
+
+
+def Q(qb, st):
+    b = 32 * qb + 4 * st
+    return f"a[{b}:{b + 3}]"
+
+
+def O(n, qb):
+    b = 64 + 16 * (2 * n + qb)
+    return f"a[{b}:{b + 15}]"
+
+
+def VSLOT(s):
+    b = 192 + 4 * s
+    return f"a[{b}:{b + 3}]", f"a[{b}:{b + 1}]", f"a[{b + 2}:{b + 3}]"
+
+
+def KSLOT(s):
+    b = 224 + 4 * s
+    return f"a[{b}:{b + 3}]"
+
+
+KADDR = [f"v{192 + st}" for st in range(8)]
+VADDR = {(n, e): f"v{200 + 2 * n + e}" for n in range(4) for e in range(2)}
+DMAK = [f"v{208 + i}" for i in range(4)]
+DMAV = [f"v{212 + i}" for i in range(4)]
+MRUN = ["v216", "v217"]
+LRUN = ["v218", "v219"]
+LIM = ["v220", "v221"]
+NINF = "v222"
+ONES = "v223"
+MX = ["v224", "v225"]
+SW = ["v226", "v227"]
+NMS = ["v228", "v229"]
+AL = ["v230", "v231"]
+ET = [f"v{232 + i}" for i in range(8)]
+BLKV = "v240"
+
+# scalar inputs
+S_KBASE, S_VBASE = "s[40:41]", "s[42:43]"
+S_KBASE_LO, S_KBASE_HI, S_VBASE_LO, S_VBASE_HI = "s40", "s41", "s42", "s43"
+S_KROW, S_VROW, S_K, S_NT, S_JM, S_BS, S_WIN, S_M0W, S_SCALE = (
+    "s44", "s45", "s46", "s47", "s48", "s49", "s50", "s51", "s52")
+# loop state
+S_J, S_LAST = "s64", "s65"
+S_B = ["s66", "s67", "s68"]        # block ids of tiles j, j+1, j+2 (paged)
+S_ROW = ["s69", "s70", "s71"]      # first cache row of tiles j, j+1, j+2
+S_KOFF, S_LB = "s72", "s73"        # key offset in block / logical block of the next block-id read
+S_RK, S_RV = "s[76:79]", "s[80:83]"  # buffer resources of the K and V fills
+S_RK_W = ["s76", "s77", "s78", "s79"]
+S_RV_W = ["s80", "s81", "s82", "s83"]
+S_F0, S_F1 = "s[84:85]", "s[86:87]"
+S_NEED = ["s[94:95]", "s[96:97]"]  # per q-block lane masks of the max update
+S_T = ["s88", "s89", "s90", "s91"]
+S_64J = "s92"
+
+LDS_V0 = 32768      # V buffer 0 (K buffers at 0 and 16384)
+TILE = 16384        # bytes of one 64-key bf16 tile
+RSRC_W3 = "0x20000"  # raw buffer: 32-bit data format, no swizzle, no stride
+
+
+class Emitter:
+    def __init__(self):
+        self.lines = []
+        self.lds = []  # outstanding LDS ops, oldest first (tags)
+
+    def __call__(self, s):
+        self.lines.append(s)
+
+    def lds_issue(self, tag, ins):
+        self.lines.append(ins)
+        self.lds.append(tag)
+
+    def lds_wait(self, tag):
+        """Wait until the LDS op `tag` has completed (LDS returns in order)."""
+        if tag not in self.lds:
+            return
+        i = self.lds.index(tag)
+        after = len(self.lds) - i - 1
+        self.lines.append(f"s_waitcnt lgkmcnt({min(after, 15)})")
+        self.lds = self.lds[i + 1:]
+
+    def lds_drain(self):
+        if self.lds:
+            self.lines.append("s_waitcnt lgkmcnt(0)")
+        self.lds = []
+
+
+# ------------------------------------------------------------- VALU lists
+def max_items(par):
+    """Row max of S_j per q-block, scaled, and the running-max update, as
+    instruction strings.  Independent chains are interleaved so no
+    instruction reads the result of the one just before it; hazard spacing
+    is built in (two wait states between a VALU write and the permlane that
+    reads it, one between an exponential and its reader).  After the
+    update, SW[qb] and MX[qb] are zero: the second and third partial row
+    sums of the exponentials, folded into l_run at the end of the tile."""
+    it = []
+    chains = [(qb, kb, MX[qb] if kb == 0 else SW[qb]) for qb in range(2) for kb in range(2)]
+    regs = {(qb, kb): [Sr(par, kb, qb, v) for v in range(16)] for qb in range(2) for kb in range(2)}
+    for qb, kb, dst in chains:
+        r = regs[(qb, kb)]
+        it.append(f"v_max3_f32 {dst}, {r[0]}, {r[1]}, {r[2]}")
+    for k in range(3, 15, 2):
+        for qb, kb, dst in chains:
+            r = regs[(qb, kb)]
+            it.append(f"v_max3_f32 {dst}, {dst}, {r[k]}, {r[k + 1]}")
+    for qb, kb, dst in chains:
+        it.append(f"v_max_f32 {dst}, {dst}, {regs[(qb, kb)][15]}")
+    for qb in range(2):
+        it.append(f"v_max_f32 {MX[qb]}, {MX[qb]}, {SW[qb]}")
+    for qb in range(2):
+        it.append(f"v_mov_b32 {SW[qb]}, {MX[qb]}")
+    it.append("s_nop 1")
+    for qb in range(2):
+        it.append(f"v_permlane32_swap_b32 {MX[qb]}, {SW[qb]}")
+    for qb in range(2):
+        it.append(f"v_max_f32 {MX[qb]}, {MX[qb]}, {SW[qb]}")
+    for qb in range(2):
+        it.append(f"v_mul_f32 {MX[qb]}, {S_SCALE}, {MX[qb]}")
+    # rescale where the tile raises the max by more than 2^8 (in log2
+    # units): need = mx > m + 8; m' = need ? mx : m; alpha = need ? 2^(m - mx) : 1
+    for qb in range(2):
+        it.append(f"v_add_f32 {SW[qb]}, 0x41000000, {MRUN[qb]}")
+    for qb in range(2):
+        it.append(f"v_sub_f32 {AL[qb]}, {MRUN[qb]}, {MX[qb]}")
+    for qb in range(2):
+        it.append(f"v_cmp_gt_f32_e64 {S_NEED[qb]}, {MX[qb]}, {SW[qb]}")
+    for qb in range(2):
+        it.append(f"v_exp_f32 {AL[qb]}, {AL[qb]}")
+    for qb in range(2):
+        it.append(f"v_cndmask_b32_e64 {MRUN[qb]}, {MRUN[qb]}, {MX[qb]}, {S_NEED[qb]}")
+    for qb in range(2):
+        it.append(f"v_cndmask_b32_e64 {AL[qb]}, 1.0, {AL[qb]}, {S_NEED[qb]}")
+    for qb in range(2):
+        it.append(f"v_xor_b32 {NMS[qb]}, 0x80000000, {MRUN[qb]}")
+    for qb in range(2):
+        it.append(f"v_cmp_eq_f32_e64 {S_NEED[qb]}, {NINF}, {MRUN[qb]}")
+    for qb in range(2):
+        it.append(f"v_mul_f32 {LRUN[qb]}, {LRUN[qb]}, {AL[qb]}")
+    for qb in range(2):
+        it.append(f"v_mov_b32 {SW[qb]}, 0")
+    for qb in range(2):
+        it.append(f"v_cndmask_b32_e64 {NMS[qb]}, {NMS[qb]}, 0, {S_NEED[qb]}")
+    for qb in range(2):
+        it.append(f"v_mov_b32 {MX[qb]}, 0")
+    it.append(f"v_cmp_neq_f32_e64 {S_F0}, 1.0, {AL[0]}")
+    it.append(f"v_cmp_neq_f32_e64 {S_F1}, 1.0, {AL[1]}")
+    return it
+
+
+def exp_pairs(par):
+    """(qb, src_a, src_b, dst P reg) for the 32 bf16 pairs of P_j: P^T slice
+    m of q-block qb holds S[m // 2][qb] registers 8 (m % 2) .. + 7."""
+    out = []
+    for qb in range(2):
+        for m in range(4):
+            for e in range(4):
+                v = 8 * (m % 2) + 2 * e
+                out.append((qb, Sr(par, m // 2, qb, v), Sr(par, m // 2, qb, v + 1), Pr(par, qb, m, e)))
+    return out
+
+
+def exp_items(pairs, k0=0):
+    """Exponentials of the pairs in groups of four: eight FMAs, eight
+    exponentials, four bf16 packs, four dot products into the three partial
+    row sums (LRUN, SW, MX) in turn, so each instruction's operands were
+    written at least three instructions earlier."""
+    it = []
+    for g0 in range(0, len(pairs), 4):
+        grp = pairs[g0:g0 + 4]
+        t = [(ET[2 * k], ET[2 * k + 1]) for k in range(len(grp))]
+        for k, (qb, a, b, p) in enumerate(grp):
+            it.append(f"v_fma_f32 {t[k][0]}, {a}, {S_SCALE}, {NMS[qb]}")
+            it.append(f"v_fma_f32 {t[k][1]}, {b}, {S_SCALE}, {NMS[qb]}")
+        for k in range(len(grp)):
+            it.append(f"v_exp_f32 {t[k][0]}, {t[k][0]}")
+            it.append(f"v_exp_f32 {t[k][1]}, {t[k][1]}")
+        for k, (qb, a, b, p) in enumerate(grp):
+            it.append(f"v_cvt_pk_bf16_f32 {p}, {t[k][0]}, {t[k][1]}")
+        for k, (qb, a, b, p) in enumerate(grp):
+            acc = (LRUN[qb], SW[qb], MX[qb])[(k0 + g0 + k) % 3]
+            it.append(f"v_dot2c_f32_bf16 {acc}, {p}, {ONES}")
+    return it
+
+
+def cost(ins):
+    if isinstance(ins, list):
+        return sum(cost(x) for x in ins)
+    if ins.startswith("v_exp"):
+        return 8
+    if ins.startswith("s_nop"):
+        return 1 + int(ins.split()[1])
+    if ins.startswith("buffer_"):
+        return 8
+    if ins.startswith("s_"):
+        return 2
+    return 4
+
+
+def spread(items, slots):
+    """Distribute items over `slots` MFMA slots by cumulative cost."""
+    total = sum(cost(i) for i in items)
+    out = [[] for _ in range(slots)]
+    acc, k = 0.0, 0
+    per = total / slots if slots else 0
+    for s in range(slots):
+        target = per * (s + 1)
+        while k < len(items) and (acc + cost(items[k]) / 2 <= target or s == slots - 1):
+            out[s].append(items[k])
+            acc += cost(items[k])
+            k += 1
+    return out
+
+
+# ------------------------------------------------------------ LDS reads
+def v_read(em, par_buf, i):
+    """V operand i (m = i // 4, n = i % 4) of the V buffer par_buf into ring slot i % 8."""
+    m, n = divmod(i, 4)
+    _, lo, hi = VSLOT(i % 8)
+    off = TILE * par_buf + 4096 * m
+    em.lds_issue(("v", i, 0), f"ds_read_b64_tr_b16 {lo}, {VADDR[(n, 0)]} offset:{off}")
+    em.lds_issue(("v", i, 1), f"ds_read_b64_tr_b16 {hi}, {VADDR[(n, 1)]} offset:{off}")
+
+
+def k_read(em, par_buf, i):
+    """K operand i (st = i // 2, kb = i % 2) of K buffer par_buf into ring slot i % 8."""
+    st, kb = divmod(i, 2)
+    off = TILE * par_buf + 8192 * kb
+    em.lds_issue(("k", i), f"ds_read_b128 {KSLOT(i % 8)}, {KADDR[st]} offset:{off}")
+
+
+def pv_mfmas(em, i, ppar):
+    m, n = divmod(i, 4)
+    slot = VSLOT(i % 8)[0]
+    return [f"{MF} {O(n, qb)}, {slot}, {P(ppar, qb, m)}, {O(n, qb)}" for qb in range(2)]
+
+
+def qk_mfmas(i, spar):
+    st, kb = divmod(i, 2)
+    slot = KSLOT(i % 8)
+    return [f"{MF} {S(spar, kb, qb)}, {slot}, {Q(qb, st)}, {S(spar, kb, qb) if st else 0}" for qb in range(2)]
+
+
+AHEAD = 4  # operands read ahead of their MFMAs
+
+
+# ------------------------------------------------------------------ fills
+def fill_tile(paged, which, row, tile, blk, par_dst):
+    """Instructions that copy one 64-key tile (K or V) into buffer par_dst:
+    row = first cache row of the tile (SGPR), tile = SGPR holding its index
+    (for the row count), blk = its block id (paged; < 0: missing).  Returns
+    a list whose items are instruction strings or groups (lists) that must
+    stay together: each m0 write, its wait state and its direct-to-LDS load."""
+    base_lo, base_hi = (S_KBASE_LO, S_KBASE_HI) if which == "k" else (S_VBASE_LO, S_VBASE_HI)
+    rowb = S_KROW if which == "k" else S_VROW
+    rs = S_RK_W if which == "k" else S_RV_W
+    rsrc = S_RK if which == "k" else S_RV
+    offs = DMAK if which == "k" else DMAV
+    t0 = S_T[0] if which == "k" else S_T[1]
+    out = [
+        f"s_mul_i32 {rs[0]}, {row}, {rowb}",
+        f"s_mul_hi_u32 {rs[1]}, {row}, {rowb}",
+        f"s_add_u32 {rs[0]}, {rs[0]}, {base_lo}",
+        f"s_addc_u32 {rs[1]}, {rs[1]}, {base_hi}",
+        f"s_and_b32 {rs[1]}, {rs[1]}, 0xffff",
+        # rows of the tile that hold keys: clamp(K - 64 t, 0, 64)
+        f"s_lshl_b32 {t0}, {tile}, 6",
+        f"s_sub_i32 {t0}, {S_K}, {t0}",
+        f"s_max_i32 {t0}, {t0}, 0",
+        f"s_min_i32 {t0}, {t0}, 64",
+        f"s_mul_i32 {rs[2]}, {t0}, {rowb}",
+    ]
+    if paged:
+        out += [f"s_cmp_lt_i32 {blk}, 0", f"s_cselect_b32 {rs[2]}, 0, {rs[2]}"]
+    out.append(f"s_mov_b32 {rs[3]}, {RSRC_W3}")
+    dst = (0 if which == "k" else LDS_V0) + TILE * par_dst
+    for i in range(4):
+        out.append([f"s_add_u32 m0, {S_M0W}, {dst + 1024 * i}", "s_nop 0",
+                    f"buffer_load_dwordx4 {offs[i]}, {rsrc}, 0 offen lds"])
+    return out
+
+
+def emit_items(em, items):
+    for x in items:
+        if isinstance(x, list):
+            for y in x:
+                em(y)
+        else:
+            em(x)
+
+
+def block_row(em, dst_row, blk):
+    """Cache row of the tile whose block id is in blk and key offset S_KOFF."""
+    em(f"s_max_i32 {S_T[2]}, {blk}, 0")
+    em(f"s_mul_i32 {dst_row}, {S_T[2]}, {S_BS}")
+    em(f"s_add_u32 {dst_row}, {dst_row}, {S_KOFF}")
+
+
+def advance_tile(em):
+    """(S_KOFF, S_LB) to the next 64-key tile."""
+    em(f"s_add_u32 {S_KOFF}, {S_KOFF}, 64")
+    em(f"s_cmp_eq_u32 {S_KOFF}, {S_BS}")
+    em(f"s_cselect_b32 {S_KOFF}, 0, {S_KOFF}")
+    em(f"s_cselect_b32 {S_T[3]}, 1, 0")
+    em(f"s_add_u32 {S_LB}, {S_LB}, {S_T[3]}")
+
+
+def read_block_id(em, tag):
+    """ds_read of the block id of logical block S_LB (window clamped)."""
+    em(f"s_min_u32 {S_T[2]}, {S_LB}, 2047")
+    em(f"s_lshl_b32 {S_T[2]}, {S_T[2]}, 2")
+    em(f"s_add_u32 {S_T[2]}, {S_T[2]}, {S_WIN}")
+    em(f"v_mov_b32 {ET[0]}, {S_T[2]}")
+    em.lds_issue(tag, f"ds_read_b32 {BLKV}, {ET[0]}")
+
+
+# ----------------------------------------------------------------- blocks
+def block_iteration(em, paged, par, first, lbl):
+    """Iteration j (parity par): fill K_{j+2}, V_j (spread over segment A);
+    segment A (PV_{j-1} unless first) beside the max / m update and the
+    first exponentials; segment B (QK_{j+1}) beside the rest; block id of
+    tile j+3; barrier."""
+    ppar, spar = 1 - par, 1 - par
+    # ---- tile rows of the fills
+    if paged:
+        em.lds_wait(("blk",))
+        em(f"v_readfirstlane_b32 {S_B[2]}, {BLKV}")
+        em("s_nop 0")
+        block_row(em, S_ROW[2], S_B[2])
+        advance_tile(em)
+    else:
+        em(f"s_add_u32 {S_T[2]}, {S_J}, 2")
+        em(f"s_lshl_b32 {S_ROW[2]}, {S_T[2]}, 6")
+    em(f"s_add_u32 {S_T[2]}, {S_J}, 2")
+    fill = fill_tile(paged, "k", S_ROW[2], S_T[2], S_B[2] if paged else None, par)
+    fill += fill_tile(paged, "v", S_ROW[0], S_J, S_B[0] if paged else None, par)
+    # ---- segment A
+    vitems = max_items(par)
+    pairs = exp_pairs(par)
+    na = 12  # exponential pairs in segment A (a multiple of 4, all of q-block 0)
+    a_items = vitems + exp_items(pairs[:na], 0)
+    b_items = exp_items(pairs[na:], na)
+    # a v_dot2c result is read by another VALU instruction three wait states later
+    b_items += ["s_nop 2"] + [f"v_add_f32 {LRUN[qb]}, {LRUN[qb]}, {SW[qb]}" for qb in range(2)]
+    b_items += [f"v_add_f32 {LRUN[qb]}, {LRUN[qb]}, {MX[qb]}" for qb in range(2)]
+    if first:
+        emit_items(em, fill)
+        emit_items(em, a_items)
+        for i in range(AHEAD):
+            k_read(em, spar, i)
+    else:
+        for i in range(AHEAD):
+            v_read(em, ppar, i)
+        lead = 8  # VALU work before the first MFMA waits for its operand
+        emit_items(em, a_items[:lead])
+        # the fill's scalar setup and loads share the first 16 slots
+        slots = spread(a_items[lead:], 32)
+        fs = spread(fill, 16)
+        for k in range(16):
+            slots[k] = fs[k] + slots[k]
+        for i in range(16):
+            em.lds_wait(("v", i, 1))
+            mf = pv_mfmas(em, i, ppar)
+            em(mf[0])
+            emit_items(em, slots[2 * i])
+            em(mf[1])
+            emit_items(em, slots[2 * i + 1])
+            if i + AHEAD < 16:
+                v_read(em, ppar, i + AHEAD)
+            else:
+                k_read(em, spar, i + AHEAD - 16)
+        # O *= alpha where the running max moved (rare)
+        em(f"s_or_b64 {S_F0}, {S_F0}, {S_F1}")
+        em(f"s_cmp_lg_u64 {S_F0}, 0")
+        em(f"s_cbranch_scc1 {lbl}_rescale")
+        em(f"{lbl}_rescaled:")
+    # ---- segment B
+    slots = spread(b_items, 32)
+    for i in range(16):
+        em.lds_wait(("k", i))
+        mf = qk_mfmas(i, spar)
+        em(mf[0])
+        emit_items(em, slots[2 * i])
+        em(mf[1])
+        emit_items(em, slots[2 * i + 1])
+        if i + AHEAD < 16:
+            k_read(em, spar, i + AHEAD)
+    # ---- next tile's mask limit, block id of tile j+3, rotation, barrier
+    em(f"v_subrev_u32 {LIM[0]}, 64, {LIM[0]}")
+    em(f"v_subrev_u32 {LIM[1]}, 64, {LIM[1]}")
+    if paged:
+        read_block_id(em, ("blk",))
+        em(f"s_mov_b32 {S_B[0]}, {S_B[1]}")
+        em(f"s_mov_b32 {S_B[1]}, {S_B[2]}")
+    em(f"s_mov_b32 {S_ROW[0]}, {S_ROW[1]}")
+    em(f"s_mov_b32 {S_ROW[1]}, {S_ROW[2]}")
+    em("s_waitcnt vmcnt(0)")
+    em("s_barrier")
+
+
+def block_rescale(em, lbl):
+    """O *= alpha per lane (both q-blocks); alpha = 1 where m did not move.
+    The PV MFMAs that wrote O were issued before the branch; 16 wait states
+    cover an 8-pass MFMA result before v_accvgpr_read."""
+    em(f"{lbl}_rescale:")
+    em("s_nop 7")
+    em("s_nop 7")
+    for r in range(16):
+        regs = [64 + 8 * r + k for k in range(8)]
+        for k, a in enumerate(regs):
+            em(f"v_accvgpr_read_b32 {ET[k]}, a{a}")
+        for k, a in enumerate(regs):
+            qb = ((a - 64) // 16) % 2
+            em(f"v_mul_f32 {ET[k]}, {ET[k]}, {AL[qb]}")
+        for k, a in enumerate(regs):
+            em(f"v_accvgpr_write_b32 a{a}, {ET[k]}")
+    em(f"s_branch {lbl}_rescaled")
+
+
+def block_mask(em, par):
+    """-inf on the scores of S_j past each row's last visible key: register v
+    of S[kb][qb] holds key 32 kb + 8 (v / 4) + v % 4 + 4 h of the tile, and
+    LIM[qb] = the lane's last visible key - 4 h.  Compares write four lane
+    masks in turn, so each v_cndmask reads a mask written four instructions
+    earlier (a VALU-written mask needs two wait states before a VALU reads it)."""
+    masks = [S_F0, S_F1, S_NEED[0], S_NEED[1]]
+    cells = [(qb, kb, v) for qb in range(2) for kb in range(2) for v in range(16)]
+    for g0 in range(0, len(cells), 4):
+        grp = cells[g0:g0 + 4]
+        for k, (qb, kb, v) in enumerate(grp):
+            c = 32 * kb + 8 * (v // 4) + (v % 4)
+            em(f"v_cmp_gt_i32_e64 {masks[k]}, {c}, {LIM[qb]}")
+        for k, (qb, kb, v) in enumerate(grp):
+            em(f"v_cndmask_b32_e64 {Sr(par, kb, qb, v)}, {Sr(par, kb, qb, v)}, {NINF}, {masks[k]}")
+
+
+def block_prologue(em, paged):
+    """State init, block ids of tiles 0..2, fills of K_0 and K_1, QK_0."""
+    em("s_nop 1")
+    for i in range(128):
+        em(f"v_accvgpr_write_b32 a{64 + i}, 0")
+    em(f"v_mov_b32 {MRUN[0]}, 0xff800000")
+    em(f"v_mov_b32 {MRUN[1]}, 0xff800000")
+    em(f"v_mov_b32 {LRUN[0]}, 0")
+    em(f"v_mov_b32 {LRUN[1]}, 0")
+    em(f"v_mov_b32 {NINF}, 0xff800000")
+    em(f"v_mov_b32 {ONES}, 0x3f803f80")
+    em(f"s_sub_u32 {S_LAST}, {S_NT}, 1")
+    em(f"s_mov_b32 {S_J}, 0")
+    if paged:
+        em(f"s_mov_b32 {S_KOFF}, 0")
+        em(f"s_mov_b32 {S_LB}, 0")
+        for t in range(2):
+            read_block_id(em, ("blk0",))
+            em.lds_drain()
+            em(f"v_readfirstlane_b32 {S_B[t]}, {BLKV}")
+            em("s_nop 0")
+            block_row(em, S_ROW[t], S_B[t])
+            advance_tile(em)
+        read_block_id(em, ("blk",))  # tile 2, taken at iteration 0
+    else:
+        em(f"s_mov_b32 {S_ROW[0]}, 0")
+        em(f"s_mov_b32 {S_ROW[1]}, 64")
+    em(f"s_mov_b32 {S_T[2]}, 0")
+    emit_items(em, fill_tile(paged, "k", S_ROW[0], S_T[2], S_B[0] if paged else None, 0))
+    em(f"s_mov_b32 {S_T[2]}, 1")
+    emit_items(em, fill_tile(paged, "k", S_ROW[1], S_T[2], S_B[1] if paged else None, 1))
+    em("s_waitcnt vmcnt(0)")
+    em("s_barrier")
+    for i in range(AHEAD):
+        k_read(em, 0, i)
+    for i in range(16):
+        em.lds_wait(("k", i))
+        for x in qk_mfmas(i, 0):
+            em(x)
+        if i + AHEAD < 16:
+            k_read(em, 0, i + AHEAD)
+    # every wave has read K_0 before iteration 0 refills its buffer; the
+    # block-id read of tile 2 is still outstanding (the wait counts it)
+    em("s_waitcnt lgkmcnt(0)")
+    em.lds = []
+    em("s_barrier")
+    em("s_nop 7")
+    em("s_nop 4")
+
+
+def block_pv_only(em, par):
+    """PV of the last tile (V and P of parity par)."""
+    for i in range(AHEAD):
+        v_read(em, par, i)
+    for i in range(16):
+        em.lds_wait(("v", i, 1))
+        for x in pv_mfmas(em, i, par):
+            em(x)
+        if i + AHEAD < 16:
+            v_read(em, par, i + AHEAD)
+    em.lds_drain()
+
+
+def program(paged):
+    em = Emitter()
+    u = "L%=_"
+    block_prologue(em, paged)
+    # iteration 0
+    em(f"s_cmp_gt_i32 {S_JM}, 0")
+    em(f"s_cbranch_scc1 {u}first")
+    block_mask(em, 0)
+    em(f"{u}first:")
+    block_iteration(em, paged, 0, True, f"{u}i0")
+    em.lds = [("blk",)] if paged else []
+    em(f"s_mov_b32 {S_J}, 1")
+    em(f"{u}top:")
+    for par in (1, 0):
+        em(f"s_cmp_gt_i32 {S_J}, {S_LAST}")
+        em(f"s_cbranch_scc1 {u}final")
+        em(f"s_cmp_lt_i32 {S_J}, {S_JM}")
+        em(f"s_cbranch_scc1 {u}nomask{par}")
+        block_mask(em, par)
+        em(f"{u}nomask{par}:")
+        block_iteration(em, paged, par, False, f"{u}f{par}")
+        em.lds = [("blk",)] if paged else []
+        em(f"s_add_u32 {S_J}, {S_J}, 1")
+    em(f"s_branch {u}top")
+    # out-of-line rescale blocks
+    for par in (1, 0):
+        block_rescale(em, f"{u}f{par}")
+    em(f"{u}final:")
+    em("s_waitcnt lgkmcnt(0)")  # the block-id read past the last tile
+    em.lds = []
+    em(f"s_bitcmp1_b32 {S_LAST}, 0")
+    em(f"s_cbranch_scc1 {u}final1")
+    block_pv_only(em, 0)
+    em(f"s_branch {u}done")
+    em(f"{u}final1:")
+    block_pv_only(em, 1)
+    em(f"{u}done:")
+    em("s_nop 7")
+    em("s_nop 7")
+    em("s_nop 3")
+    return em.lines
+
+
+CLOBBERS = (
+    [f"v{i}" for i in range(0, 192)] + ["v216", "v217"] + [f"v{i}" for i in range(222, 241)]
+    + [f"a{i}" for i in range(192, 256)] + [f"s{i}" for i in range(64, 98)]
+    + ["vcc", "scc", "m0", "memory"]
+)
+
+
+def render(name, lines):
+    out = [f"#define {name} \\"]
+    for ln in lines:
+        out.append(f'  "{ln}\\n" \\')
+    out.append('  ""')
+    return "\n".join(out)
+
+
+def main():
+    here = os.path.dirname(os.path.abspath(__file__))
+    paged = program(True)
+    local = program(False)
+    clob = ", ".join(f'"{c}"' for c in CLOBBERS)
+    text = [
+        "// Generated by gen_prefill_mx.py; do not edit by hand.",
+        "// The tile loop of one prefill work item (see paged_prefill_mx.hip).",
+        "#pragma once",
+        "",
+        render("NVS_PREFILL_MX_ASM_PAGED", paged),
+        "",
+        render("NVS_PREFILL_MX_ASM_LOCAL", local),
+        "",
+        f"#define NVS_PREFILL_MX_CLOBBERS {clob}",
+        "",
+    ]
+    path = os.path.join(here, "prefill_mx_asm.inc")
+    with open(path, "w") as f:
+        f.write("\n".join(text))
+    print(f"wrote {path}: {len(paged)} + {len(local)} lines", file=sys.stderr)
+
+
+if __name__ == "__main__":
+    main()
