@@ -56,10 +56,12 @@ def _compile(src: Path) -> Path:
 
 
 def generate() -> None:
-    """Regenerate the prefill kernel's tile loop (csrc/prefill_mx_asm.inc)."""
-    res = subprocess.run([sys.executable, str(CSRC / "gen_prefill_mx.py")], capture_output=True, text=True)
-    if res.returncode != 0:
-        raise RuntimeError(f"gen_prefill_mx.py failed:\n{res.stderr}")
+    """Regenerate the prefill kernel's tile loop (csrc/prefill_mx_asm.inc) and
+    check that every register it writes is declared to the compiler."""
+    for script in ("gen_prefill_mx.py", "check_prefill_mx.py"):
+        res = subprocess.run([sys.executable, str(CSRC / script)], capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"{script} failed:\n{res.stdout}{res.stderr}")
 
 
 def build(verbose: bool = True) -> Path:

@@ -221,28 +221,38 @@ def exp_pairs(par):
 
 def exp_items(pairs, k0=0):
     """Exponentials of the pairs in groups of four: eight FMAs, eight
-    exponentials, four bf16 packs, four dot products into the three partial
-    row sums (LRUN, SW, MX) in turn, so each instruction's operands were
-    written at least three instructions earlier."""
+    exponentials, four bf16 packs, then the row sums in fp32 (the values
+    before rounding, as a flash softmax keeps its row sum): two adds fold
+    the eight values of the group into two of the three partial sums
+    (LRUN, SW, MX) in turn.  Each instruction's operands were written at
+    least two instructions earlier (v_dot2c, which would sum the packed
+    values, shares the matrix pipe and stalls the MFMAs)."""
     it = []
     for g0 in range(0, len(pairs), 4):
         grp = pairs[g0:g0 + 4]
+        qb = grp[0][0]
         t = [(ET[2 * k], ET[2 * k + 1]) for k in range(len(grp))]
-        for k, (qb, a, b, p) in enumerate(grp):
+        for k, (_, a, b, p) in enumerate(grp):
             it.append(f"v_fma_f32 {t[k][0]}, {a}, {S_SCALE}, {NMS[qb]}")
             it.append(f"v_fma_f32 {t[k][1]}, {b}, {S_SCALE}, {NMS[qb]}")
         for k in range(len(grp)):
             it.append(f"v_exp_f32 {t[k][0]}, {t[k][0]}")
             it.append(f"v_exp_f32 {t[k][1]}, {t[k][1]}")
-        for k, (qb, a, b, p) in enumerate(grp):
+        for k, (_, a, b, p) in enumerate(grp):
             it.append(f"v_cvt_pk_bf16_f32 {p}, {t[k][0]}, {t[k][1]}")
-        for k, (qb, a, b, p) in enumerate(grp):
-            acc = (LRUN[qb], SW[qb], MX[qb])[(k0 + g0 + k) % 3]
-            it.append(f"v_dot2c_f32_bf16 {acc}, {p}, {ONES}")
+        # t0 + t1 -> t0, t2 + t3 -> t2, ... then two partial sums
+        for k in range(len(grp)):
+            it.append(f"v_add_f32 {t[k][0]}, {t[k][0]}, {t[k][1]}")
+        acc = [(LRUN[qb], SW[qb], MX[qb])[(k0 + g0 + m) % 3] for m in range(2)]
+        it.append(f"v_add_f32 {t[0][0]}, {t[0][0]}, {t[1][0]}")
+        it.append(f"v_add_f32 {t[2][0]}, {t[2][0]}, {t[3][0]}")
+        it.append(f"v_add_f32 {acc[0]}, {acc[0]}, {t[0][0]}")
+        it.append(f"v_add_f32 {acc[1]}, {acc[1]}, {t[2][0]}")
     return it
 
 
 def cost(ins):
+    """Issue cycles of an instruction beside MFMAs (measured on gfx950)."""
     if isinstance(ins, list):
         return sum(cost(x) for x in ins)
     if ins.startswith("v_exp"):
@@ -301,6 +311,17 @@ def qk_mfmas(i, spar):
 
 
 AHEAD = 4  # operands read ahead of their MFMAs
+
+# Optional callback mark(em, k) at the phase boundaries of an iteration
+# (k = 0 after the tile rows, 1 after segment A, 2 after segment B, 3 after
+# the fills' wait, 4 after the barrier), after the prologue (5), at the end
+# (6) and mark(em, None) at the start of the program; None in the product.
+MARK = None
+
+
+def mark(em, k):
+    if MARK is not None:
+        MARK(em, k)
 
 
 # ------------------------------------------------------------------ fills
@@ -391,6 +412,7 @@ def block_iteration(em, paged, par, first, lbl):
         em(f"s_add_u32 {S_T[2]}, {S_J}, 2")
         em(f"s_lshl_b32 {S_ROW[2]}, {S_T[2]}, 6")
     em(f"s_add_u32 {S_T[2]}, {S_J}, 2")
+    mark(em, 0)
     fill = fill_tile(paged, "k", S_ROW[2], S_T[2], S_B[2] if paged else None, par)
     fill += fill_tile(paged, "v", S_ROW[0], S_J, S_B[0] if paged else None, par)
     # ---- segment A
@@ -399,12 +421,12 @@ def block_iteration(em, paged, par, first, lbl):
     na = 12  # exponential pairs in segment A (a multiple of 4, all of q-block 0)
     a_items = vitems + exp_items(pairs[:na], 0)
     b_items = exp_items(pairs[na:], na)
-    # a v_dot2c result is read by another VALU instruction three wait states later
-    b_items += ["s_nop 2"] + [f"v_add_f32 {LRUN[qb]}, {LRUN[qb]}, {SW[qb]}" for qb in range(2)]
+    b_items += [f"v_add_f32 {LRUN[qb]}, {LRUN[qb]}, {SW[qb]}" for qb in range(2)]
     b_items += [f"v_add_f32 {LRUN[qb]}, {LRUN[qb]}, {MX[qb]}" for qb in range(2)]
     if first:
         emit_items(em, fill)
         emit_items(em, a_items)
+        mark(em, 1)
         for i in range(AHEAD):
             k_read(em, spar, i)
     else:
@@ -433,6 +455,7 @@ def block_iteration(em, paged, par, first, lbl):
         em(f"s_cmp_lg_u64 {S_F0}, 0")
         em(f"s_cbranch_scc1 {lbl}_rescale")
         em(f"{lbl}_rescaled:")
+        mark(em, 1)
     # ---- segment B
     slots = spread(b_items, 32)
     for i in range(16):
@@ -444,6 +467,7 @@ def block_iteration(em, paged, par, first, lbl):
         emit_items(em, slots[2 * i + 1])
         if i + AHEAD < 16:
             k_read(em, spar, i + AHEAD)
+    mark(em, 2)
     # ---- next tile's mask limit, block id of tile j+3, rotation, barrier
     em(f"v_subrev_u32 {LIM[0]}, 64, {LIM[0]}")
     em(f"v_subrev_u32 {LIM[1]}, 64, {LIM[1]}")
@@ -454,7 +478,9 @@ def block_iteration(em, paged, par, first, lbl):
     em(f"s_mov_b32 {S_ROW[0]}, {S_ROW[1]}")
     em(f"s_mov_b32 {S_ROW[1]}, {S_ROW[2]}")
     em("s_waitcnt vmcnt(0)")
+    mark(em, 3)
     em("s_barrier")
+    mark(em, 4)
 
 
 def block_rescale(em, lbl):
@@ -539,6 +565,7 @@ def block_prologue(em, paged):
     em("s_waitcnt lgkmcnt(0)")
     em.lds = []
     em("s_barrier")
+    mark(em, 5)
     em("s_nop 7")
     em("s_nop 4")
 
@@ -559,6 +586,7 @@ def block_pv_only(em, par):
 def program(paged):
     em = Emitter()
     u = "L%=_"
+    mark(em, None)
     block_prologue(em, paged)
     # iteration 0
     em(f"s_cmp_gt_i32 {S_JM}, 0")
@@ -593,6 +621,7 @@ def program(paged):
     em(f"{u}final1:")
     block_pv_only(em, 1)
     em(f"{u}done:")
+    mark(em, 6)
     em("s_nop 7")
     em("s_nop 7")
     em("s_nop 3")
