@@ -310,7 +310,19 @@ def qk_mfmas(i, spar):
     return [f"{MF} {S(spar, kb, qb)}, {slot}, {Q(qb, st)}, {S(spar, kb, qb) if st else 0}" for qb in range(2)]
 
 
-AHEAD = 4  # operands read ahead of their MFMAs
+AHEAD = 6  # operands read ahead of their MFMAs (at most 7: the rings hold 8)
+READ_EARLY = True  # issue each read-ahead right after the slot's first MFMA
+V_FIRST = True  # issue segment A's first V reads before the fills' set-up
+NA = 12  # exponential pairs of segment A
+
+
+def read_ahead_a(em, ppar, spar, i):
+    """Segment A's read-ahead after PV operand i: V operand i + AHEAD, or,
+    in the last AHEAD slots, the first K operands of segment B."""
+    if i + AHEAD < 16:
+        v_read(em, ppar, i + AHEAD)
+    else:
+        k_read(em, spar, i + AHEAD - 16)
 
 # Optional callback mark(em, k) at the phase boundaries of an iteration
 # (k = 0 after the tile rows, 1 after segment A, 2 after segment B, 3 after
@@ -401,6 +413,9 @@ def block_iteration(em, paged, par, first, lbl):
     first exponentials; segment B (QK_{j+1}) beside the rest; block id of
     tile j+3; barrier."""
     ppar, spar = 1 - par, 1 - par
+    if V_FIRST and not first:
+        for i in range(AHEAD):
+            v_read(em, ppar, i)
     # ---- tile rows of the fills
     if paged:
         em.lds_wait(("blk",))
@@ -418,7 +433,7 @@ def block_iteration(em, paged, par, first, lbl):
     # ---- segment A
     vitems = max_items(par)
     pairs = exp_pairs(par)
-    na = 12  # exponential pairs in segment A (a multiple of 4, all of q-block 0)
+    na = NA  # exponential pairs in segment A (a multiple of 4, all of q-block 0)
     a_items = vitems + exp_items(pairs[:na], 0)
     b_items = exp_items(pairs[na:], na)
     b_items += [f"v_add_f32 {LRUN[qb]}, {LRUN[qb]}, {SW[qb]}" for qb in range(2)]
@@ -430,8 +445,9 @@ def block_iteration(em, paged, par, first, lbl):
         for i in range(AHEAD):
             k_read(em, spar, i)
     else:
-        for i in range(AHEAD):
-            v_read(em, ppar, i)
+        if not V_FIRST:
+            for i in range(AHEAD):
+                v_read(em, ppar, i)
         lead = 8  # VALU work before the first MFMA waits for its operand
         emit_items(em, a_items[:lead])
         # the fill's scalar setup and loads share the first 16 slots
@@ -443,13 +459,13 @@ def block_iteration(em, paged, par, first, lbl):
             em.lds_wait(("v", i, 1))
             mf = pv_mfmas(em, i, ppar)
             em(mf[0])
+            if READ_EARLY:
+                read_ahead_a(em, ppar, spar, i)
             emit_items(em, slots[2 * i])
             em(mf[1])
             emit_items(em, slots[2 * i + 1])
-            if i + AHEAD < 16:
-                v_read(em, ppar, i + AHEAD)
-            else:
-                k_read(em, spar, i + AHEAD - 16)
+            if not READ_EARLY:
+                read_ahead_a(em, ppar, spar, i)
         # O *= alpha where the running max moved (rare)
         em(f"s_or_b64 {S_F0}, {S_F0}, {S_F1}")
         em(f"s_cmp_lg_u64 {S_F0}, 0")
@@ -462,10 +478,12 @@ def block_iteration(em, paged, par, first, lbl):
         em.lds_wait(("k", i))
         mf = qk_mfmas(i, spar)
         em(mf[0])
+        if READ_EARLY and i + AHEAD < 16:
+            k_read(em, spar, i + AHEAD)
         emit_items(em, slots[2 * i])
         em(mf[1])
         emit_items(em, slots[2 * i + 1])
-        if i + AHEAD < 16:
+        if not READ_EARLY and i + AHEAD < 16:
             k_read(em, spar, i + AHEAD)
     mark(em, 2)
     # ---- next tile's mask limit, block id of tile j+3, rotation, barrier
