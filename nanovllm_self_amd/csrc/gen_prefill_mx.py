@@ -93,6 +93,7 @@ NMS = ["v228", "v229"]
 AL = ["v230", "v231"]
 ET = [f"v{232 + i}" for i in range(8)]
 BLKV = "v240"
+X3 = ["v241", "v242"]  # third partial row sum
 
 # scalar inputs
 S_KBASE, S_VBASE = "s[40:41]", "s[42:43]"
@@ -108,7 +109,8 @@ S_RK, S_RV = "s[76:79]", "s[80:83]"  # buffer resources of the K and V fills
 S_RK_W = ["s76", "s77", "s78", "s79"]
 S_RV_W = ["s80", "s81", "s82", "s83"]
 S_F0, S_F1 = "s[84:85]", "s[86:87]"
-S_NEED = ["s[94:95]", "s[96:97]"]  # per q-block lane masks of the max update
+S_NEED = ["s[94:95]", "s[96:97]"]  # per q-block lane masks (temporaries)
+S_MINF = "s[98:99]"  # lanes whose running max is still -inf (no visible key yet)
 S_T = ["s88", "s89", "s90", "s91"]
 S_64J = "s92"
 
@@ -145,14 +147,16 @@ class Emitter:
 
 
 # ------------------------------------------------------------- VALU lists
-def max_items(par):
-    """Row max of S_j per q-block, scaled, and the running-max update, as
+# the row sums of a tile may reach SUM_LIMIT before the running max moves:
+# no exponential of a tile exceeds 2^16 times the row's running max term
+SUM_LIMIT = "0x47800000"  # 65536.0
+
+
+def row_max(par):
+    """MX[qb] = scale * (max of the lane's row over the tile's 64 keys), as
     instruction strings.  Independent chains are interleaved so no
-    instruction reads the result of the one just before it; hazard spacing
-    is built in (two wait states between a VALU write and the permlane that
-    reads it, one between an exponential and its reader).  After the
-    update, SW[qb] and MX[qb] are zero: the second and third partial row
-    sums of the exponentials, folded into l_run at the end of the tile."""
+    instruction reads the result of the one just before it; two wait states
+    separate the VALU writes from the permlane that reads them."""
     it = []
     chains = [(qb, kb, MX[qb] if kb == 0 else SW[qb]) for qb in range(2) for kb in range(2)]
     regs = {(qb, kb): [Sr(par, kb, qb, v) for v in range(16)] for qb in range(2) for kb in range(2)}
@@ -176,34 +180,39 @@ def max_items(par):
         it.append(f"v_max_f32 {MX[qb]}, {MX[qb]}, {SW[qb]}")
     for qb in range(2):
         it.append(f"v_mul_f32 {MX[qb]}, {S_SCALE}, {MX[qb]}")
-    # rescale where the tile raises the max by more than 2^8 (in log2
-    # units): need = mx > m + 8; m' = need ? mx : m; alpha = need ? 2^(m - mx) : 1
+    return it
+
+
+def max_update(first):
+    """Running max m <- max(m, MX) (first tile: m <- MX), exponent offset
+    NMS = -m (0 where m is -inf, so masked scores give exp2(-inf) = 0), the
+    lanes still at -inf in S_MINF and, after the first tile, alpha =
+    2^(m_old - m_new) in AL (1 where m is -inf) with l_run *= alpha.  One
+    wait state follows each exponential before its reader and two each
+    v_cmp before the v_cndmask that reads its mask."""
+    it = []
+    if not first:
+        for qb in range(2):
+            it.append(f"v_max_f32 {MX[qb]}, {MX[qb]}, {MRUN[qb]}")
+        for qb in range(2):
+            it.append(f"v_sub_f32 {AL[qb]}, {MRUN[qb]}, {MX[qb]}")
     for qb in range(2):
-        it.append(f"v_add_f32 {SW[qb]}, 0x41000000, {MRUN[qb]}")
+        it.append(f"v_cmp_eq_f32_e64 {S_NEED[qb]}, {NINF}, {MX[qb]}")
+    if not first:
+        for qb in range(2):
+            it.append(f"v_exp_f32 {AL[qb]}, {AL[qb]}")
     for qb in range(2):
-        it.append(f"v_sub_f32 {AL[qb]}, {MRUN[qb]}, {MX[qb]}")
+        it.append(f"v_mov_b32 {MRUN[qb]}, {MX[qb]}")
     for qb in range(2):
-        it.append(f"v_cmp_gt_f32_e64 {S_NEED[qb]}, {MX[qb]}, {SW[qb]}")
-    for qb in range(2):
-        it.append(f"v_exp_f32 {AL[qb]}, {AL[qb]}")
-    for qb in range(2):
-        it.append(f"v_cndmask_b32_e64 {MRUN[qb]}, {MRUN[qb]}, {MX[qb]}, {S_NEED[qb]}")
-    for qb in range(2):
-        it.append(f"v_cndmask_b32_e64 {AL[qb]}, 1.0, {AL[qb]}, {S_NEED[qb]}")
-    for qb in range(2):
-        it.append(f"v_xor_b32 {NMS[qb]}, 0x80000000, {MRUN[qb]}")
-    for qb in range(2):
-        it.append(f"v_cmp_eq_f32_e64 {S_NEED[qb]}, {NINF}, {MRUN[qb]}")
-    for qb in range(2):
-        it.append(f"v_mul_f32 {LRUN[qb]}, {LRUN[qb]}, {AL[qb]}")
-    for qb in range(2):
-        it.append(f"v_mov_b32 {SW[qb]}, 0")
+        it.append(f"v_xor_b32 {NMS[qb]}, 0x80000000, {MX[qb]}")
     for qb in range(2):
         it.append(f"v_cndmask_b32_e64 {NMS[qb]}, {NMS[qb]}, 0, {S_NEED[qb]}")
-    for qb in range(2):
-        it.append(f"v_mov_b32 {MX[qb]}, 0")
-    it.append(f"v_cmp_neq_f32_e64 {S_F0}, 1.0, {AL[0]}")
-    it.append(f"v_cmp_neq_f32_e64 {S_F1}, 1.0, {AL[1]}")
+    if not first:
+        for qb in range(2):
+            it.append(f"v_cndmask_b32_e64 {AL[qb]}, {AL[qb]}, 1.0, {S_NEED[qb]}")
+        for qb in range(2):
+            it.append(f"v_mul_f32 {LRUN[qb]}, {LRUN[qb]}, {AL[qb]}")
+    it.append(f"s_or_b64 {S_MINF}, {S_NEED[0]}, {S_NEED[1]}")
     return it
 
 
@@ -219,18 +228,21 @@ def exp_pairs(par):
     return out
 
 
-def exp_items(pairs, k0=0):
+def exp_items(pairs, k0, touched):
     """Exponentials of the pairs in groups of four: eight FMAs, eight
-    exponentials, four bf16 packs, then the row sums in fp32 (the values
-    before rounding, as a flash softmax keeps its row sum): two adds fold
-    the eight values of the group into two of the three partial sums
-    (LRUN, SW, MX) in turn.  Each instruction's operands were written at
-    least two instructions earlier (v_dot2c, which would sum the packed
-    values, shares the matrix pipe and stalls the MFMAs)."""
+    exponentials, four bf16 packs, then the tile's row sums in fp32 (the
+    values before rounding, as a flash softmax keeps its row sum): the
+    eight values of a group go into two of the three partial sums (SW, MX,
+    X3) in turn; a partial's first write of the tile is a move.
+    `touched` collects (qb, partial) across the calls of one tile.  Each
+    instruction's operands were written at least two instructions earlier
+    (v_dot2c, which would sum the packed values, shares the matrix pipe and
+    stalls the MFMAs)."""
     it = []
     for g0 in range(0, len(pairs), 4):
         grp = pairs[g0:g0 + 4]
         qb = grp[0][0]
+        assert all(x[0] == qb for x in grp) and len(grp) == 4
         t = [(ET[2 * k], ET[2 * k + 1]) for k in range(len(grp))]
         for k, (_, a, b, p) in enumerate(grp):
             it.append(f"v_fma_f32 {t[k][0]}, {a}, {S_SCALE}, {NMS[qb]}")
@@ -243,11 +255,23 @@ def exp_items(pairs, k0=0):
         # t0 + t1 -> t0, t2 + t3 -> t2, ... then two partial sums
         for k in range(len(grp)):
             it.append(f"v_add_f32 {t[k][0]}, {t[k][0]}, {t[k][1]}")
-        acc = [(LRUN[qb], SW[qb], MX[qb])[(k0 + g0 + m) % 3] for m in range(2)]
         it.append(f"v_add_f32 {t[0][0]}, {t[0][0]}, {t[1][0]}")
         it.append(f"v_add_f32 {t[2][0]}, {t[2][0]}, {t[3][0]}")
-        it.append(f"v_add_f32 {acc[0]}, {acc[0]}, {t[0][0]}")
-        it.append(f"v_add_f32 {acc[1]}, {acc[1]}, {t[2][0]}")
+        for m, src in enumerate((t[0][0], t[2][0])):
+            j = (k0 + g0 + m) % 3
+            acc = (SW[qb], MX[qb], X3[qb])[j]
+            if (qb, j) in touched:
+                it.append(f"v_add_f32 {acc}, {acc}, {src}")
+            else:
+                touched.add((qb, j))
+                it.append(f"v_mov_b32 {acc}, {src}")
+    return it
+
+
+def tile_sum_items():
+    """SW[qb] <- the tile's row sum of the lane (the three partials)."""
+    it = [f"v_add_f32 {SW[qb]}, {SW[qb]}, {MX[qb]}" for qb in range(2)]
+    it += [f"v_add_f32 {SW[qb]}, {SW[qb]}, {X3[qb]}" for qb in range(2)]
     return it
 
 
@@ -431,13 +455,13 @@ def block_iteration(em, paged, par, first, lbl):
     fill = fill_tile(paged, "k", S_ROW[2], S_T[2], S_B[2] if paged else None, par)
     fill += fill_tile(paged, "v", S_ROW[0], S_J, S_B[0] if paged else None, par)
     # ---- segment A
-    vitems = max_items(par)
     pairs = exp_pairs(par)
-    na = NA  # exponential pairs in segment A (a multiple of 4, all of q-block 0)
-    a_items = vitems + exp_items(pairs[:na], 0)
-    b_items = exp_items(pairs[na:], na)
-    b_items += [f"v_add_f32 {LRUN[qb]}, {LRUN[qb]}, {SW[qb]}" for qb in range(2)]
-    b_items += [f"v_add_f32 {LRUN[qb]}, {LRUN[qb]}, {MX[qb]}" for qb in range(2)]
+    na = NA  # exponential pairs in segment A (a multiple of 4)
+    touched = set()
+    a_items = (row_max(par) + max_update(True)) if first else []
+    a_items += exp_items(pairs[:na], 0, touched)
+    b_items = exp_items(pairs[na:], na, touched) + tile_sum_items()
+    assert len(touched) == 6, "every partial row sum is written each tile"
     if first:
         emit_items(em, fill)
         emit_items(em, a_items)
@@ -466,11 +490,6 @@ def block_iteration(em, paged, par, first, lbl):
             emit_items(em, slots[2 * i + 1])
             if not READ_EARLY:
                 read_ahead_a(em, ppar, spar, i)
-        # O *= alpha where the running max moved (rare)
-        em(f"s_or_b64 {S_F0}, {S_F0}, {S_F1}")
-        em(f"s_cmp_lg_u64 {S_F0}, 0")
-        em(f"s_cbranch_scc1 {lbl}_rescale")
-        em(f"{lbl}_rescaled:")
         mark(em, 1)
     # ---- segment B
     slots = spread(b_items, 32)
@@ -485,6 +504,16 @@ def block_iteration(em, paged, par, first, lbl):
         emit_items(em, slots[2 * i + 1])
         if not READ_EARLY and i + AHEAD < 16:
             k_read(em, spar, i + AHEAD)
+    # The tile's row sums, taken with the running max of the tiles before:
+    # past SUM_LIMIT or not finite (a max that was stale or still -inf) on
+    # any lane, the slow path redoes the tile with its own max.
+    em(f"v_add_f32 {ET[0]}, {SW[0]}, {SW[1]}")
+    em(f"v_cmp_nge_f32 vcc, {SUM_LIMIT}, {ET[0]}")
+    em(f"s_or_b64 vcc, vcc, {S_MINF}")
+    em(f"s_cbranch_scc1 {lbl}_slow")
+    for qb in range(2):
+        em(f"v_add_f32 {LRUN[qb]}, {LRUN[qb]}, {SW[qb]}")
+    em(f"{lbl}_summed:")
     mark(em, 2)
     # ---- next tile's mask limit, block id of tile j+3, rotation, barrier
     em(f"v_subrev_u32 {LIM[0]}, 64, {LIM[0]}")
@@ -501,11 +530,19 @@ def block_iteration(em, paged, par, first, lbl):
     mark(em, 4)
 
 
-def block_rescale(em, lbl):
-    """O *= alpha per lane (both q-blocks); alpha = 1 where m did not move.
-    The PV MFMAs that wrote O were issued before the branch; 16 wait states
-    cover an 8-pass MFMA result before v_accvgpr_read."""
-    em(f"{lbl}_rescale:")
+def block_slow(em, par, lbl):
+    """Slow path of tile j (parity par), out of line: the running max moves
+    to the tile's max, l_run and (where alpha != 1 on some lane) O scale by
+    alpha, and P_j and the tile's row sums are redone with the new max.  The
+    PV MFMAs that wrote O were issued a segment earlier; 16 wait states
+    cover an MFMA result before v_accvgpr_read regardless."""
+    em(f"{lbl}_slow:")
+    emit_items(em, row_max(par))
+    emit_items(em, max_update(False))
+    em(f"v_cmp_neq_f32_e64 {S_F0}, 1.0, {AL[0]}")
+    em(f"v_cmp_neq_f32_e64 {S_F1}, 1.0, {AL[1]}")
+    em(f"s_or_b64 {S_F0}, {S_F0}, {S_F1}")
+    em(f"s_cbranch_scc0 {lbl}_scaled")
     em("s_nop 7")
     em("s_nop 7")
     for r in range(16):
@@ -517,7 +554,13 @@ def block_rescale(em, lbl):
             em(f"v_mul_f32 {ET[k]}, {ET[k]}, {AL[qb]}")
         for k, a in enumerate(regs):
             em(f"v_accvgpr_write_b32 a{a}, {ET[k]}")
-    em(f"s_branch {lbl}_rescaled")
+    em(f"{lbl}_scaled:")
+    touched = set()
+    emit_items(em, exp_items(exp_pairs(par), 0, touched))
+    emit_items(em, tile_sum_items())
+    for qb in range(2):
+        em(f"v_add_f32 {LRUN[qb]}, {LRUN[qb]}, {SW[qb]}")
+    em(f"s_branch {lbl}_summed")
 
 
 def block_mask(em, par):
@@ -626,9 +669,10 @@ def program(paged):
         em.lds = [("blk",)] if paged else []
         em(f"s_add_u32 {S_J}, {S_J}, 1")
     em(f"s_branch {u}top")
-    # out-of-line rescale blocks
+    # out-of-line slow paths
+    block_slow(em, 0, f"{u}i0")
     for par in (1, 0):
-        block_rescale(em, f"{u}f{par}")
+        block_slow(em, par, f"{u}f{par}")
     em(f"{u}final:")
     em("s_waitcnt lgkmcnt(0)")  # the block-id read past the last tile
     em.lds = []
@@ -647,8 +691,8 @@ def program(paged):
 
 
 CLOBBERS = (
-    [f"v{i}" for i in range(0, 192)] + ["v216", "v217"] + [f"v{i}" for i in range(222, 241)]
-    + [f"a{i}" for i in range(192, 256)] + [f"s{i}" for i in range(64, 98)]
+    [f"v{i}" for i in range(0, 192)] + ["v216", "v217"] + [f"v{i}" for i in range(222, 243)]
+    + [f"a{i}" for i in range(192, 256)] + [f"s{i}" for i in range(64, 100)]
     + ["vcc", "scc", "m0", "memory"]
 )
 

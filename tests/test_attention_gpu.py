@@ -228,6 +228,38 @@ def test_rows_without_keys_are_zero(device):
     compare(got, ref.numpy(), False, "rows without keys")
 
 
+def test_rows_without_keys_multi_tile(device):
+    """q_len > k_len over several 64-key tiles: rows 0 .. 99 see no key (0),
+    the rest see a growing prefix; waves hold both kinds of rows."""
+    say("rows without keys, multi-tile")
+    tabs = _tables([300], 4, 17)
+    wl = _custom([SeqSlice(tabs[0], 0, 300)], 8, 2, 4, seed=17)
+    wl.context.cu_seqlens_k = torch.tensor([0, 200], dtype=torch.int32, device=device)
+    wl.context.max_seqlen_k = 200
+    wl.context.block_tables = torch.tensor([tabs[0]], dtype=torch.int32, device=device)
+    got = _run(wl)
+    assert np.all(got[:100] == 0)
+    kk, vv = [x.reshape(-1, 2, 128)[:200] for x in cache_blocks_f32(wl.attn, np.asarray(tabs[0]))]
+    ref = AO.attention_cached(torch.from_numpy(bf16_to_np(wl.q)), torch.from_numpy(kk)[None],
+                              torch.from_numpy(vv)[None], [0, 300], [0, 200], 8, 2, 128)
+    compare(got, ref.numpy(), False, "rows without keys, multi-tile")
+
+
+@pytest.mark.parametrize("prefix", [0, 256])
+def test_prefill_scores_jump_in_later_tiles(device, prefix):
+    """Keys of later tiles scaled by 8 and 32: the running max of every row
+    jumps by far more than the tile loop lets it lag, twice, after rows have
+    accumulated earlier tiles (the max moves and O / l rescale mid-row)."""
+    say(f"prefill score jumps, prefix {prefix}")
+    L = 700
+    tabs = _tables([prefix + L], 8, 18)
+    wl = _custom([SeqSlice(tabs[0], prefix, L)], 8, 2, 8, seed=18)
+    with torch.no_grad():
+        wl.k[320:384] *= 8
+        wl.k[520:600] *= 32
+    _check(wl, what=f"prefill score jumps/{prefix}")
+
+
 # ---------------------------------------------------------------- mixed
 @pytest.mark.parametrize("kv", ["bf16", "fp8"])
 def test_mixed_small(device, kv):
