@@ -98,8 +98,10 @@ X3 = ["v241", "v242"]  # third partial row sum
 # scalar inputs
 S_KBASE, S_VBASE = "s[40:41]", "s[42:43]"
 S_KBASE_LO, S_KBASE_HI, S_VBASE_LO, S_VBASE_HI = "s40", "s41", "s42", "s43"
-S_KROW, S_VROW, S_K, S_NT, S_JM, S_BS, S_WIN, S_M0W, S_SCALE = (
+S_KROW, S_VROW, S_K, S_NT, S_JM, S_BS, S_NB, S_M0W, S_SCALE = (
     "s44", "s45", "s46", "s47", "s48", "s49", "s50", "s51", "s52")
+S_RBT = "s[36:39]"  # buffer resource of the sequence's block-table row (paged)
+S_RBT_NREC = "s38"  # its size in bytes: 4 x the blocks of the sequence
 # loop state
 S_J, S_LAST = "s64", "s65"
 S_B = ["s66", "s67", "s68"]        # block ids of tiles j, j+1, j+2 (paged)
@@ -112,7 +114,7 @@ S_F0, S_F1 = "s[84:85]", "s[86:87]"
 S_NEED = ["s[94:95]", "s[96:97]"]  # per q-block lane masks (temporaries)
 S_MINF = "s[98:99]"  # lanes whose running max is still -inf (no visible key yet)
 S_T = ["s88", "s89", "s90", "s91"]
-S_64J = "s92"
+S_BOK = "s93"  # 1 if the block-id load in flight is of a block of the sequence
 
 LDS_V0 = 32768      # V buffer 0 (K buffers at 0 and 16384)
 TILE = 16384        # bytes of one 64-key bf16 tile
@@ -421,32 +423,45 @@ def advance_tile(em):
     em(f"s_add_u32 {S_LB}, {S_LB}, {S_T[3]}")
 
 
-def read_block_id(em, tag):
-    """ds_read of the block id of logical block S_LB (window clamped)."""
-    em(f"s_min_u32 {S_T[2]}, {S_LB}, 2047")
-    em(f"s_lshl_b32 {S_T[2]}, {S_T[2]}, 2")
-    em(f"s_add_u32 {S_T[2]}, {S_T[2]}, {S_WIN}")
+def issue_block_id(em):
+    """Vector load of the block id of logical block S_LB into BLKV (every
+    lane the same address); S_BOK records whether S_LB is a block of the
+    sequence.  The loop's vmcnt(0) before each barrier completes it."""
+    em(f"s_lshl_b32 {S_T[2]}, {S_LB}, 2")
     em(f"v_mov_b32 {ET[0]}, {S_T[2]}")
-    em.lds_issue(tag, f"ds_read_b32 {BLKV}, {ET[0]}")
+    em(f"buffer_load_dword {BLKV}, {ET[0]}, {S_RBT}, 0 offen")
+    em(f"s_cmp_lt_u32 {S_T[2]}, {S_RBT_NREC}")
+    em(f"s_cselect_b32 {S_BOK}, 1, 0")
+
+
+def take_block_id(em, dst):
+    """dst <- the block id loaded by issue_block_id, or -1 where the
+    logical block is past the sequence's or the id is outside the pool."""
+    em(f"v_readfirstlane_b32 {dst}, {BLKV}")
+    em("s_nop 0")
+    em(f"s_cmp_lt_u32 {dst}, {S_NB}")
+    em(f"s_cselect_b32 {dst}, {dst}, -1")
+    em(f"s_cmp_eq_u32 {S_BOK}, 0")
+    em(f"s_cselect_b32 {dst}, -1, {dst}")
 
 
 # ----------------------------------------------------------------- blocks
 def block_iteration(em, paged, par, first, lbl):
     """Iteration j (parity par): fill K_{j+2}, V_j (spread over segment A);
     segment A (PV_{j-1} unless first) beside the max / m update and the
-    first exponentials; segment B (QK_{j+1}) beside the rest; block id of
-    tile j+3; barrier."""
+    first exponentials; segment B (QK_{j+1}) beside the rest; the row-sum
+    check; barrier.  Paged: the block id of tile j+2 (loaded an iteration
+    earlier) is taken first and the load of tile j+3's issued."""
     ppar, spar = 1 - par, 1 - par
     if V_FIRST and not first:
         for i in range(AHEAD):
             v_read(em, ppar, i)
     # ---- tile rows of the fills
     if paged:
-        em.lds_wait(("blk",))
-        em(f"v_readfirstlane_b32 {S_B[2]}, {BLKV}")
-        em("s_nop 0")
+        take_block_id(em, S_B[2])
         block_row(em, S_ROW[2], S_B[2])
         advance_tile(em)
+        issue_block_id(em)  # tile j+3, taken at iteration j+1
     else:
         em(f"s_add_u32 {S_T[2]}, {S_J}, 2")
         em(f"s_lshl_b32 {S_ROW[2]}, {S_T[2]}, 6")
@@ -515,11 +530,10 @@ def block_iteration(em, paged, par, first, lbl):
         em(f"v_add_f32 {LRUN[qb]}, {LRUN[qb]}, {SW[qb]}")
     em(f"{lbl}_summed:")
     mark(em, 2)
-    # ---- next tile's mask limit, block id of tile j+3, rotation, barrier
+    # ---- next tile's mask limit, rotation, barrier
     em(f"v_subrev_u32 {LIM[0]}, 64, {LIM[0]}")
     em(f"v_subrev_u32 {LIM[1]}, 64, {LIM[1]}")
     if paged:
-        read_block_id(em, ("blk",))
         em(f"s_mov_b32 {S_B[0]}, {S_B[1]}")
         em(f"s_mov_b32 {S_B[1]}, {S_B[2]}")
     em(f"s_mov_b32 {S_ROW[0]}, {S_ROW[1]}")
@@ -597,13 +611,12 @@ def block_prologue(em, paged):
         em(f"s_mov_b32 {S_KOFF}, 0")
         em(f"s_mov_b32 {S_LB}, 0")
         for t in range(2):
-            read_block_id(em, ("blk0",))
-            em.lds_drain()
-            em(f"v_readfirstlane_b32 {S_B[t]}, {BLKV}")
-            em("s_nop 0")
+            issue_block_id(em)
+            em("s_waitcnt vmcnt(0)")
+            take_block_id(em, S_B[t])
             block_row(em, S_ROW[t], S_B[t])
             advance_tile(em)
-        read_block_id(em, ("blk",))  # tile 2, taken at iteration 0
+        issue_block_id(em)  # tile 2, taken at iteration 0
     else:
         em(f"s_mov_b32 {S_ROW[0]}, 0")
         em(f"s_mov_b32 {S_ROW[1]}, 64")
@@ -621,8 +634,7 @@ def block_prologue(em, paged):
             em(x)
         if i + AHEAD < 16:
             k_read(em, 0, i + AHEAD)
-    # every wave has read K_0 before iteration 0 refills its buffer; the
-    # block-id read of tile 2 is still outstanding (the wait counts it)
+    # every wave has read K_0 before iteration 0 refills its buffer
     em("s_waitcnt lgkmcnt(0)")
     em.lds = []
     em("s_barrier")
@@ -655,7 +667,7 @@ def program(paged):
     block_mask(em, 0)
     em(f"{u}first:")
     block_iteration(em, paged, 0, True, f"{u}i0")
-    em.lds = [("blk",)] if paged else []
+    em.lds = []
     em(f"s_mov_b32 {S_J}, 1")
     em(f"{u}top:")
     for par in (1, 0):
@@ -666,7 +678,7 @@ def program(paged):
         block_mask(em, par)
         em(f"{u}nomask{par}:")
         block_iteration(em, paged, par, False, f"{u}f{par}")
-        em.lds = [("blk",)] if paged else []
+        em.lds = []
         em(f"s_add_u32 {S_J}, {S_J}, 1")
     em(f"s_branch {u}top")
     # out-of-line slow paths
@@ -674,7 +686,7 @@ def program(paged):
     for par in (1, 0):
         block_slow(em, par, f"{u}f{par}")
     em(f"{u}final:")
-    em("s_waitcnt lgkmcnt(0)")  # the block-id read past the last tile
+    em("s_waitcnt vmcnt(0) lgkmcnt(0)")  # no load may land after the asm
     em.lds = []
     em(f"s_bitcmp1_b32 {S_LAST}, 0")
     em(f"s_cbranch_scc1 {u}final1")
@@ -683,6 +695,14 @@ def program(paged):
     em(f"{u}final1:")
     block_pv_only(em, 1)
     em(f"{u}done:")
+    # l_run of the lane's row over both key halves (lanes l and l ^ 32)
+    for qb in range(2):
+        em(f"v_mov_b32 {ET[qb]}, {LRUN[qb]}")
+    em("s_nop 1")
+    for qb in range(2):
+        em(f"v_permlane32_swap_b32 {LRUN[qb]}, {ET[qb]}")
+    for qb in range(2):
+        em(f"v_add_f32 {LRUN[qb]}, {LRUN[qb]}, {ET[qb]}")
     mark(em, 6)
     em("s_nop 7")
     em("s_nop 7")
