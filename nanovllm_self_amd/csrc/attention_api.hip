@@ -67,7 +67,7 @@ int64_t attention_workspace_bytes(int num_seqs, int max_seqlen_q, int max_seqlen
 // so the workspace sized for it holds either plan.
 static Plan make_plan(void* ws, const AttnParams& P) {
   const int pbm = prefill_mx_serves(P) ? prefill_mx_positions(P.Hq / P.Hkv) : prefill_pbm(P.Hq, P.Hkv);
-  return plan_at(ws, prefill_tiles(P.max_seqlen_q, pbm), pbm);
+  return plan_at(ws, P.B, prefill_tiles(P.max_seqlen_q, pbm), pbm);
 }
 
 static int launch_prefill_any(const AttnParams& P, const Plan& plan, hipStream_t s) {

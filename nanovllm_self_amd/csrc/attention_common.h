@@ -100,11 +100,20 @@ struct PlanHeader {
 };
 static_assert(sizeof(PlanHeader) == 256, "plan header is one 256-byte line");
 
+// What a work-group of the MFMA prefill kernel needs to start a list entry,
+// in one 32-byte load: the entry, its sequence's query and key ranges and
+// (paged) the block ids of its first three 64-key tiles (-1: missing).
+struct PlanRecord {
+  int item, q0, L, k0, K, blk0, blk1, blk2;
+};
+static_assert(sizeof(PlanRecord) == 32, "plan record is 32 bytes");
+
 struct Plan {
   PlanHeader* hdr;
   int* plist;
-  int ntq;  // prefill query tiles per sequence (list stride)
-  int pbm;  // query positions per prefill tile
+  PlanRecord* rec;  // per list entry, beside plist
+  int ntq;          // prefill query tiles per sequence (list stride)
+  int pbm;          // query positions per prefill tile
 };
 
 inline int64_t align256(int64_t x) { return (x + 255) & ~(int64_t)255; }
@@ -125,13 +134,15 @@ inline int decode_wave_cap(int B, int max_seqlen_k, int Hkv) {
 
 // Bytes of the plan for a batch; it sits at the start of the workspace.
 inline int64_t plan_bytes(int B, int ntq) {
-  return (int64_t)sizeof(PlanHeader) + align256((int64_t)B * ntq * 4);
+  return (int64_t)sizeof(PlanHeader) + align256((int64_t)B * ntq * 4) +
+         align256((int64_t)B * ntq * (int64_t)sizeof(PlanRecord));
 }
 
-inline Plan plan_at(void* ws, int ntq, int pbm) {
+inline Plan plan_at(void* ws, int B, int ntq, int pbm) {
   Plan p;
   p.hdr = (PlanHeader*)ws;
   p.plist = (int*)((char*)ws + sizeof(PlanHeader));
+  p.rec = (PlanRecord*)((char*)ws + sizeof(PlanHeader) + align256((int64_t)B * ntq * 4));
   p.ntq = ntq;
   p.pbm = pbm;
   return p;

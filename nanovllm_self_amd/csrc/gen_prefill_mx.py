@@ -102,6 +102,7 @@ S_KROW, S_VROW, S_K, S_NT, S_JM, S_BS, S_NB, S_M0W, S_SCALE = (
     "s44", "s45", "s46", "s47", "s48", "s49", "s50", "s51", "s52")
 S_RBT = "s[36:39]"  # buffer resource of the sequence's block-table row (paged)
 S_RBT_NREC = "s38"  # its size in bytes: 4 x the blocks of the sequence
+S_BLK012 = ["s33", "s34", "s35"]  # block ids of tiles 0, 1, 2 (paged; from the plan)
 # loop state
 S_J, S_LAST = "s64", "s65"
 S_B = ["s66", "s67", "s68"]        # block ids of tiles j, j+1, j+2 (paged)
@@ -451,14 +452,18 @@ def block_iteration(em, paged, par, first, lbl):
     segment A (PV_{j-1} unless first) beside the max / m update and the
     first exponentials; segment B (QK_{j+1}) beside the rest; the row-sum
     check; barrier.  Paged: the block id of tile j+2 (loaded an iteration
-    earlier) is taken first and the load of tile j+3's issued."""
+    earlier; iteration 0: from the plan) is taken first and the load of
+    tile j+3's issued."""
     ppar, spar = 1 - par, 1 - par
     if V_FIRST and not first:
         for i in range(AHEAD):
             v_read(em, ppar, i)
     # ---- tile rows of the fills
     if paged:
-        take_block_id(em, S_B[2])
+        if first:
+            em(f"s_mov_b32 {S_B[2]}, {S_BLK012[2]}")
+        else:
+            take_block_id(em, S_B[2])
         block_row(em, S_ROW[2], S_B[2])
         advance_tile(em)
         issue_block_id(em)  # tile j+3, taken at iteration j+1
@@ -595,7 +600,11 @@ def block_mask(em, par):
 
 
 def block_prologue(em, paged):
-    """State init, block ids of tiles 0..2, fills of K_0 and K_1, QK_0."""
+    """State init, block ids of tiles 0 and 1 (inputs), QK_0.  K_0 and K_1
+    are in the K buffers when the loop starts (the caller copies them in
+    while the previous unit ends).  No vector memory op is issued here: the
+    caller's prefetch of the next unit's query rows may still be in flight,
+    and the first wait on vmcnt is the one that ends iteration 0."""
     em("s_nop 1")
     for i in range(128):
         em(f"v_accvgpr_write_b32 a{64 + i}, 0")
@@ -611,21 +620,12 @@ def block_prologue(em, paged):
         em(f"s_mov_b32 {S_KOFF}, 0")
         em(f"s_mov_b32 {S_LB}, 0")
         for t in range(2):
-            issue_block_id(em)
-            em("s_waitcnt vmcnt(0)")
-            take_block_id(em, S_B[t])
+            em(f"s_mov_b32 {S_B[t]}, {S_BLK012[t]}")
             block_row(em, S_ROW[t], S_B[t])
             advance_tile(em)
-        issue_block_id(em)  # tile 2, taken at iteration 0
     else:
         em(f"s_mov_b32 {S_ROW[0]}, 0")
         em(f"s_mov_b32 {S_ROW[1]}, 64")
-    em(f"s_mov_b32 {S_T[2]}, 0")
-    emit_items(em, fill_tile(paged, "k", S_ROW[0], S_T[2], S_B[0] if paged else None, 0))
-    em(f"s_mov_b32 {S_T[2]}, 1")
-    emit_items(em, fill_tile(paged, "k", S_ROW[1], S_T[2], S_B[1] if paged else None, 1))
-    em("s_waitcnt vmcnt(0)")
-    em("s_barrier")
     for i in range(AHEAD):
         k_read(em, 0, i)
     for i in range(16):

@@ -11,8 +11,22 @@ struct PlanArgs {
   int B;
   int64_t T;
   int paged;
+  const int32_t* bt;  // paged: block tables
+  int64_t bt_stride;
+  int64_t NB;
+  int bs;
   Plan plan;
 };
+
+// Block id of the tile of keys [64 t, 64 t + 64) of row b: -1 past the
+// row's blocks or outside the pool.
+__device__ __forceinline__ int tile_block(const PlanArgs& a, int b, int kl, int t) {
+  const int lb = 64 * t / a.bs;
+  const int64_t nblk = min((int64_t)(kl + a.bs - 1) / a.bs, a.bt_stride);
+  if (lb >= nblk) return -1;
+  const int blk = a.bt[(int64_t)b * a.bt_stride + lb];
+  return (blk >= 0 && blk < a.NB) ? blk : -1;
+}
 
 // Inclusive scan of one int per thread over the 1024-thread work-group:
 // shuffle scan inside each wave, then the 16 wave totals through LDS.  Also
@@ -74,7 +88,23 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanArgs a) {
     int np, q0, kl, tot;
     row_work(a, b0 + tid, dec, np, q0, kl);
     const int incl = block_scan_1024(np, scan_lds, tot);
-    for (int i = 0; i < np; ++i) pl.plist[base + incl - np + i] = (b0 + tid) * pl.ntq + (np - 1 - i);
+    if (np > 0) {
+      const int b = b0 + tid, k0 = a.cu_k[b];
+      PlanRecord r;
+      r.q0 = q0;
+      r.L = a.cu_q[b + 1] - q0;
+      r.k0 = k0;
+      r.K = kl;
+      r.blk0 = a.paged ? tile_block(a, b, kl, 0) : -1;
+      r.blk1 = a.paged ? tile_block(a, b, kl, 1) : -1;
+      r.blk2 = a.paged ? tile_block(a, b, kl, 2) : -1;
+      for (int i = 0; i < np; ++i) {
+        const int e = base + incl - np + i;
+        r.item = b * pl.ntq + (np - 1 - i);
+        pl.plist[e] = r.item;
+        pl.rec[e] = r;
+      }
+    }
     base += tot;
   }
   if (tid == 0) pl.hdr->n_prefill = base;
@@ -101,6 +131,10 @@ int launch_plan(const AttnParams& P, const Plan& plan, bool paged, hipStream_t s
   a.B = P.B;
   a.T = P.T;
   a.paged = paged ? 1 : 0;
+  a.bt = P.bt;
+  a.bt_stride = P.bt_stride;
+  a.NB = P.NB;
+  a.bs = P.bs > 0 ? P.bs : 64;
   a.plan = plan;
   hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(1024), 0, stream, a);
   return check_launch("plan");
