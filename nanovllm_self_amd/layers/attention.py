@@ -263,6 +263,14 @@ class PagedAttention(nn.Module):
         store_slots the same call first writes k / v to those cache slots
         (nvs_paged_attention_store, paged mode only)."""
         compute = torch.bfloat16
+        # The reference also computes in fp16 (attention_compute_dtype float16,
+        # attention.py:22-23, 327-330); these kernels compute in bf16 only, so
+        # fp16 is refused in both modes rather than rounded to bf16.
+        if self.attention_compute_dtype == torch.float16 or q.dtype == torch.float16 or (
+                context.block_tables is None and (k.dtype == torch.float16 or v.dtype == torch.float16)):
+            raise RuntimeError(
+                "HIP attention computes in bf16: fp16 attention (attention_compute_dtype float16 or fp16 "
+                "q/k/v) is not served")
         if q.dtype != compute:
             q = q.to(compute)
         _need_device(q, "q")

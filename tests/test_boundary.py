@@ -157,6 +157,23 @@ def test_dtype_mismatch_guard():
         a.prefill_flashattn(z, z, z, context=None)
 
 
+@pytest.mark.parametrize("paged", [False, True])
+def test_fp16_attention_is_refused_in_both_modes(paged):
+    """fp16 compute is not served: local mode (block_tables None) and paged
+    mode both raise instead of rounding q/k/v to bf16."""
+    a = PagedAttention(8, 8, 128)
+    a.block_size = 256
+    a.k_cache = torch.zeros(1, 256, 8, 128, dtype=torch.float16)
+    a.v_cache = torch.zeros_like(a.k_cache)
+    a.kv_cache_dtype = a.attention_compute_dtype = torch.float16
+    z = torch.zeros(1, 8, 128, dtype=torch.float16)
+    cu = torch.tensor([0, 1], dtype=torch.int32)
+    ctx = Context(cu_seqlens_q=cu, cu_seqlens_k=cu, max_seqlen_q=1, max_seqlen_k=1,
+                  block_tables=torch.zeros(1, 1, dtype=torch.int32) if paged else None)
+    with pytest.raises(RuntimeError, match="fp16 attention"):
+        a.prefill_flashattn(z, z, z, ctx)
+
+
 def test_no_cpu_fallback():
     a = PagedAttention(8, 8, 128)
     a.block_size = 256
