@@ -12,7 +12,8 @@ sequences, new U[512, 4096] over 0-8 cached blocks, seed 2), quantised
 decode tokens/s (256 sequences, ctx U[1024, 4096], fp8 / int8 / bf16, seed
 3), the mixed chunked-prefill + decode step at a Qwen3-32B-like shape (seed
 4), the dominant kernel's roofline fraction (HIP events on the launch
-stream), the CPU eager restatement timed on the host cores, and the steps
+stream), the CPU eager restatement timed on the host cores beside each of
+those workloads (with the CPU model and count), and the steps
 either side of the path: the fused q/k norm + rotary + KV store
 (`qk_prep`), the step's Context built on the device (`step_context`) and
 the KV handoff block copies (`kv_handoff`).
@@ -67,7 +68,7 @@ def step(wl):
     return lambda: wl.attn.forward(wl.q, wl.k, wl.v, wl.context)
 
 
-def bench_decode(steps, warmup):
+def bench_decode(steps, warmup, cpu=False):
     from nanovllm_self_amd import workloads as W
 
     log("building decode_8b (bf16)")
@@ -97,6 +98,9 @@ def bench_decode(steps, warmup):
     }
     log(f"decode_small: eager {ms_small * 1e3:.1f} us/step (wall {wall * 1e3:.1f}), "
         f"graph {res['small_step']['graph_ms_per_step'] * 1e3:.1f} us/step")
+    if cpu:
+        log("cpu baseline: decode_small")
+        res["small_step"]["cpu_baseline"] = cpu_decode_leg(small, 3.0, "decode_small", full_passes=3)
     del small
     return wl, res
 
@@ -125,7 +129,7 @@ def graph_step_ms(wl, steps, warmup):
     return ms
 
 
-def bench_prefill(steps, warmup):
+def bench_prefill(steps, warmup, cpu=False):
     from nanovllm_self_amd import workloads as W
 
     log("building prefill_8b")
@@ -143,11 +147,14 @@ def bench_prefill(steps, warmup):
         "tokens_per_s": sum(s.num_new_tokens for s in wl.seqs) / (ms_step / 1e3),
     }
     log(f"prefill_8b: attention {ms_attn:.3f} ms -> {res['tflops']:.0f} TFLOP/s")
+    if cpu:
+        log("cpu baseline: prefill_8b")
+        res["cpu_baseline"] = cpu_prefill_leg(wl, 10.0, "prefill_8b")
     del wl
     return res
 
 
-def bench_quant(steps, warmup):
+def bench_quant(steps, warmup, cpu=False):
     from nanovllm_self_amd import workloads as W
 
     out = {"workload": "decode_quant: 32q/8kv heads, D128, bs256, 256 seqs, ctx U[1024,4096], 1% outliers x8, seed 3"}
@@ -165,6 +172,9 @@ def bench_quant(steps, warmup):
             "tokens_per_s": wl.num_seqs / (ms_step / 1e3),
         }
         log(f"decode_quant/{kv}: {ms_step:.3f} ms/step -> {out[kv]['tokens_per_s']:.0f} tok/s")
+        if cpu and kv != "bf16":
+            log(f"cpu baseline: decode_quant/{kv}")
+            out[kv]["cpu_baseline"] = cpu_decode_leg(wl, 5.0, f"decode_quant/{kv}", dequant_timed=True)
         del wl
         torch.cuda.empty_cache()
     out["fp8_vs_bf16_tokens"] = out["fp8"]["tokens_per_s"] / out["bf16"]["tokens_per_s"]
@@ -366,7 +376,7 @@ def bench_handoff(steps, warmup):
     return out
 
 
-def bench_mixed(steps, warmup):
+def bench_mixed(steps, warmup, cpu=False):
     from nanovllm_self_amd import workloads as W
 
     out = {"workload": "mixed_32b: 64q/8kv heads, 128 decode seqs ctx logU[256,32768] + 4 x 2048-token chunks over U[0,16384] cached, 16384 blocks, seed 4"}
@@ -384,6 +394,16 @@ def bench_mixed(steps, warmup):
             "frac_roofline": t_roof * 1e3 / ms_step,
         }
         log(f"mixed_32b/{kv}: {ms_step:.3f} ms/step (roofline {t_roof * 1e3:.3f} ms)")
+        if cpu and kv == "bf16":
+            log("cpu baseline: mixed_32b")
+            dec = cpu_decode_leg(wl, 6.0, "mixed_32b decode part")
+            pre = cpu_prefill_leg(wl, 6.0, "mixed_32b prefill part")
+            ms = (dec_b / (dec["value"] * 1e9) + pf / (pre["value"] * 1e12)) * 1e3
+            out[kv]["cpu_baseline"] = dict(
+                value=round(ms, 1), unit="ms per step (extrapolated from the two parts' rates)",
+                cores=dec["cores"], kind="port", decode_part=dec, prefill_part=pre,
+                sample="decode rows and prefill row blocks as sampled below, each rate applied to the "
+                       "step's decode bytes / prefill FLOPs", **cpu_host())
         del wl
         torch.cuda.empty_cache()
     return out
@@ -398,40 +418,151 @@ def cpu_threads() -> int:
         return os.cpu_count() or 1
 
 
-def cpu_baseline(wl, budget_s: float = 10.0):
-    """The eager restatement (gather + per-sequence fp32 attention, the
-    reference's torch path) on the host cores, over a bounded sample of the
-    decode batch: whole passes over the batch's sequences, repeated until
-    about `budget_s` seconds of CPU work are done.  Unit: decode bytes / s,
-    the GPU figure's unit."""
-    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
-    from oracle import attn_oracle
-    from tests.gpu_util import oracle_paged_inputs
+def cpu_host():
+    """The host CPU's model name (/proc/cpuinfo, as lscpu reports it) and its
+    logical CPU count."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.lower().startswith("model name"):
+                    model = ln.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "os_cpu_count": os.cpu_count()}
 
+
+def _cpu_setup():
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     torch.set_num_threads(cpu_threads())
+
+
+def _host_seq(wl, i, dequant_timed=False):
+    """Sequence i's query rows and cache blocks in host memory (untimed: the
+    CPU path, like the GPU one, starts from resident data).  With
+    dequant_timed, a quantised cache stays as codes and scales and the
+    returned `prepare` dequantises them (the eager path's dequantize step,
+    timed with the attention); otherwise `prepare` is the identity."""
+    import numpy as np
+    from oracle import kv_oracle as KO
+    from tests.gpu_util import bf16_to_np, oracle_paged_inputs
+
+    args, _ = oracle_paged_inputs(wl, [i])
+    if not (dequant_timed and wl.kv != "bf16"):
+        return args, lambda a: a
+    s = wl.seqs[i]
+    n = s.num_cached_tokens + s.num_new_tokens
+    idx = torch.as_tensor(s.block_table[:(n + wl.block_size - 1) // wl.block_size], dtype=torch.long,
+                          device=wl.attn.k_cache.device)
+    raw = []
+    for cache, scale in ((wl.attn.k_cache, wl.attn.k_scale_cache), (wl.attn.v_cache, wl.attn.v_scale_cache)):
+        codes = cache.index_select(0, idx).cpu().view(torch.uint8).numpy()
+        if wl.kv == "int8":
+            codes = codes.view(np.int8)
+        raw.append((codes, scale.index_select(0, idx).cpu().numpy()))
+
+    def prepare(a):
+        kv = [KO.round_to_bf16(KO.dequantize_per_token(c, sc, wl.kv)) for c, sc in raw]
+        return (a[0], kv[0], kv[1]) + tuple(a[3:])
+
+    return args, prepare
+
+
+def cpu_decode_leg(wl, budget_s, label, dequant_timed=False, full_passes=0):
+    """Decode rows through the eager restatement on the host cores: per
+    sequence, (dequantise,) gather and fp32 attention, in batch order, until
+    about `budget_s` seconds (with full_passes > 0: whole passes over the
+    batch, at least that many, the rate taken over all of them).  Units: the
+    GPU figures' units, decode bytes / s and decode rows (tokens) / s."""
+    from oracle import attn_oracle
+
+    _cpu_setup()
+    ids = list(wl.decode_seq_ids())
+    ctx = [wl.seqs[i].num_cached_tokens + wl.seqs[i].num_new_tokens for i in ids]
     H, D, Hq = wl.num_kv_heads, wl.head_dim, wl.num_heads
-    # Inputs are brought to host memory first (untimed): the CPU path, like
-    # the GPU one, starts from resident data.
-    inputs = [oracle_paged_inputs(wl, [i])[0] for i in range(wl.num_seqs)]
-    attn_oracle.paged_attention(*inputs[0])  # warm-up
-    nbytes, seqs, t = 0, 0, 0.0
-    while t < budget_s and seqs < 64 * wl.num_seqs:
-        i = seqs % wl.num_seqs
-        ctx = wl.seqs[i].num_cached_tokens + wl.seqs[i].num_new_tokens
-        t0 = time.perf_counter()
-        attn_oracle.paged_attention(*inputs[i])
-        t += time.perf_counter() - t0
-        nbytes += ctx * H * 2 * D * 2 + Hq * D * 2 * 2
-        seqs += 1
-    del inputs
-    return {
-        "value": round(nbytes / t / 1e9, 4),
-        "unit": "GB/s",
-        "cores": torch.get_num_threads(),
-        "kind": "port",
-        "sample": f"decode_8b, {seqs} sequence decodes in batch order ({nbytes / 1e9:.2f} GB of K/V/q/o), "
-                  f"{t:.1f} s: per-sequence gather + fp32 attention from host memory",
-    }
+    s_kv, s_sc = (2, 0) if wl.kv == "bf16" else (1, 4)
+    seq_bytes = [c * H * 2 * (D * s_kv + s_sc) + Hq * D * 2 * 2 for c in ctx]
+    keep = {}
+    nbytes, rows, t, passes, stop = 0, 0, 0.0, 0, False
+    while not stop:
+        for j, i in enumerate(ids):
+            args, prep = keep[i] if i in keep else _host_seq(wl, i, dequant_timed)
+            if full_passes:
+                keep[i] = (args, prep)
+            if rows == 0:  # warm-up
+                attn_oracle.paged_attention(*prep(args))
+            t0 = time.perf_counter()
+            attn_oracle.paged_attention(*prep(args))
+            t += time.perf_counter() - t0
+            nbytes += seq_bytes[j]
+            rows += 1
+            if t >= budget_s and not full_passes:
+                stop = True
+                break
+        else:
+            passes += 1
+            stop = stop or (full_passes and passes >= full_passes and t >= budget_s)
+    keep.clear()
+    if full_passes:
+        what = f"{passes} full passes over the batch's {len(ids)} rows"
+    elif rows > len(ids):
+        what = f"{rows} rows: the batch's {len(ids)} rows in order, repeated"
+    else:
+        what = f"the first {rows} of the batch's {len(ids)} rows"
+    sample = (f"{label}: {what}, {nbytes / 1e9:.2f} GB, {t:.1f} s: per row "
+              + ("dequantise + " if dequant_timed and wl.kv != "bf16" else "")
+              + "gather + fp32 attention from host memory")
+    return dict(value=round(nbytes / t / 1e9, 4), unit="GB/s", tokens_per_s=round(rows / t, 2),
+                cores=torch.get_num_threads(), kind="port", sample=sample, **cpu_host())
+
+
+def cpu_prefill_leg(wl, budget_s, label, rows_per_block=256):
+    """Prefill rows through the eager restatement on the host cores, in
+    blocks of query rows: a row block [r0, r1) of a sequence with P cached
+    tokens is the same attention as a sequence of r1 - r0 new tokens over
+    P + r1 keys, so the sample is whole row blocks of the batch's sequences,
+    in order, until about `budget_s` seconds.  Unit: TFLOP/s counted as the
+    GPU figure counts them (4 Hq D per visible query-key pair)."""
+    from oracle import attn_oracle
+
+    _cpu_setup()
+    Hq, D = wl.num_heads, wl.head_dim
+    flops, t, nblk = 0.0, 0.0, 0
+    warm = False
+    for i in wl.prefill_seq_ids():
+        s = wl.seqs[i]
+        P, L = s.num_cached_tokens, s.num_new_tokens
+        args, _ = _host_seq(wl, i)
+        q = args[0]
+        for r0 in range(0, L, rows_per_block):
+            r1 = min(L, r0 + rows_per_block)
+            klen = P + r1
+            blk = (q[r0:r1], args[1], args[2], args[3], [0, r1 - r0], [0, klen], [klen]) + tuple(args[7:])
+            if not warm:
+                attn_oracle.paged_attention(*blk)
+                warm = True
+            t0 = time.perf_counter()
+            attn_oracle.paged_attention(*blk)
+            t += time.perf_counter() - t0
+            flops += 4.0 * Hq * D * ((r1 - r0) * P + (r1 * (r1 + 1) - r0 * (r0 + 1)) // 2)
+            nblk += 1
+            if t >= budget_s:
+                break
+        if t >= budget_s:
+            break
+    sample = (f"{label}: {nblk} blocks of up to {rows_per_block} query rows, sequences in batch order, "
+              f"{flops / 1e12:.3f} TFLOP, {t:.1f} s: per block gather + fp32 attention with the "
+              f"bottom-right causal mask, from host memory")
+    return dict(value=round(flops / t / 1e12, 5), unit="TFLOP/s", cores=torch.get_num_threads(), kind="port",
+                sample=sample, **cpu_host())
+
+
+def cpu_baseline(wl, budget_s: float = 10.0):
+    """The headline's CPU leg: decode_8b rows through the eager restatement
+    (gather + per-sequence fp32 attention, the reference's torch path) on
+    the host cores.  Unit: decode bytes / s, the GPU figure's unit."""
+    return cpu_decode_leg(wl, budget_s, "decode_8b")
 
 
 def decode_traffic():
@@ -503,7 +634,8 @@ def main():
         print(json.dumps(bench_handoff(steps, warmup)))
         return
 
-    wl, dec = bench_decode(steps, warmup)
+    want_cpu = args.only is None and not args.no_cpu
+    wl, dec = bench_decode(steps, warmup, cpu=want_cpu)
     line = {
         "metric": "paged-decode attn GB/s (%HBM peak) + prefill attn TFLOP/s, Qwen3-8B shape",
         "value": round(dec["gbs_step"], 2),
@@ -541,9 +673,9 @@ def main():
             line["cpu_baseline"] = cpu_baseline(wl)
         del wl
         torch.cuda.empty_cache()
-        line["prefill_8b"] = bench_prefill(max(5, steps // 4), 2)
-        line["decode_quant"] = bench_quant(steps, warmup)
-        line["mixed_32b"] = bench_mixed(max(5, steps // 4), 2)
+        line["prefill_8b"] = bench_prefill(steps, warmup, cpu=want_cpu)
+        line["decode_quant"] = bench_quant(steps, warmup, cpu=want_cpu)
+        line["mixed_32b"] = bench_mixed(steps, warmup, cpu=want_cpu)
         line["qk_prep"] = bench_prep(steps, warmup)
         line["step_context"] = bench_context(steps, warmup)
         line["kv_handoff"] = bench_handoff(steps, warmup)
