@@ -15,10 +15,12 @@ decode tokens/s (256 sequences, ctx U[1024, 4096], fp8 / int8 / bf16, seed
 stream), the CPU eager restatement timed on the host cores beside each of
 those workloads (with the CPU model and count), and the steps
 either side of the path: the fused q/k norm + rotary + KV store
-(`qk_prep`), the step's Context built on the device (`step_context`) and
-the KV handoff block copies (`kv_handoff`).
+(`qk_prep`), the step's Context built on the device (`step_context`), the
+KV handoff block copies (`kv_handoff`) and a 36-layer decode step, eager
+against one HIP-graph replay (`layers36_decode_step`).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only decode|prefill|quant|mixed|prep|context|handoff]
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+                    [--only decode|prefill|quant|mixed|prep|context|handoff|layers]
 """
 from __future__ import annotations
 
@@ -127,6 +129,78 @@ def graph_step_ms(wl, steps, warmup):
         attn.in_cuda_graph_capture = False
     _, ms = timed_steps(graph.replay, steps, warmup)
     return ms
+
+
+def bench_layers(steps, warmup, n_layers=36):
+    """A decode step of a whole model's attention: n_layers PagedAttention
+    layers (Qwen3-8B has 36), each with its own K/V in one pool, each doing
+    its store + decode on the step's batch in turn; eager (one forward call
+    per layer) against one replay of the whole step captured in a HIP graph.
+    Wall clock and HIP events; the difference is the inter-token latency the
+    graph saves at that batch size."""
+    from nanovllm_self_amd import PagedAttention
+    from nanovllm_self_amd import workloads as W
+    from nanovllm_self_amd.kv_cache import KVCacheConfig, allocate_kv_cache, bind_kv_cache
+    from nanovllm_self_amd.layers.attention import reserve_attention_workspace
+
+    out = {"n_layers": n_layers}
+    for name, build in (("decode_small", W.decode_small), ("decode_8b", W.decode_8b)):
+        log(f"building {n_layers}-layer {name}")
+        wl = build("cuda")
+        ctx, a0 = wl.context, wl.attn
+        # Every layer's own slice of one pool when it fits in 64 GiB, else
+        # the layers share the workload's pool (same bytes read per layer).
+        per_layer = a0.k_cache.numel() * a0.k_cache.element_size() * 2
+        cfg = KVCacheConfig(dtype=torch.bfloat16, kv_cache_dtype=torch.bfloat16,
+                            attention_compute_dtype=torch.bfloat16, block_size=wl.block_size,
+                            num_blocks=wl.num_blocks)
+        layers = [PagedAttention(wl.num_heads, wl.num_kv_heads, wl.head_dim, dtype=torch.bfloat16)
+                  for _ in range(n_layers)]
+        own = per_layer * n_layers <= (64 << 30)
+        if own:
+            pool, _ = allocate_kv_cache(n_layers, wl.num_kv_heads, wl.head_dim, cfg, "cuda")
+            pool[:, :] = torch.stack([a0.k_cache, a0.v_cache]).unsqueeze(1)
+            bind_kv_cache(layers, pool, None, cfg)
+        else:
+            pool = torch.stack([a0.k_cache, a0.v_cache]).unsqueeze(1).expand(2, n_layers, *a0.k_cache.shape)
+            bind_kv_cache(layers, pool, None, cfg)
+
+        def eager():
+            for layer in layers:
+                layer.forward(wl.q, wl.k, wl.v, ctx)
+
+        wall_e, ms_e = timed_steps(eager, steps, warmup)
+        reserve_attention_workspace(wl.num_seqs, int(ctx.max_seqlen_q), int(ctx.max_seqlen_k), wl.num_heads,
+                                    wl.q.device, num_kv_heads=wl.num_kv_heads)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            eager()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        for layer in layers:
+            layer.in_cuda_graph_capture = True
+        try:
+            with torch.cuda.graph(graph):
+                eager()
+        finally:
+            for layer in layers:
+                layer.in_cuda_graph_capture = False
+        wall_g, ms_g = timed_steps(graph.replay, steps, warmup)
+        out[name] = {
+            "kv_per_layer": "own" if own else "shared pool",
+            "eager_wall_ms_per_step": wall_e,
+            "eager_ms_per_step": ms_e,
+            "graph_wall_ms_per_step": wall_g,
+            "graph_ms_per_step": ms_g,
+            "itl_saved_ms": wall_e - wall_g,
+        }
+        log(f"{n_layers} layers {name}: eager {wall_e:.3f} ms wall ({ms_e:.3f} events), graph {wall_g:.3f} ms wall "
+            f"({ms_g:.3f} events)")
+        del graph, layers, pool, wl
+        torch.cuda.empty_cache()
+    return out
 
 
 def bench_prefill(steps, warmup, cpu=False):
@@ -594,7 +668,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", choices=["decode", "prefill", "quant", "mixed", "prep", "context", "handoff"], default=None)
+    ap.add_argument("--only", choices=["decode", "prefill", "quant", "mixed", "prep", "context", "handoff", "layers"],
+                    default=None)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--calib-copy", action="store_true",
                     help="only run a 1 GiB device copy (for scaling PMC byte counters)")
@@ -632,6 +707,9 @@ def main():
         return
     if args.only == "handoff":
         print(json.dumps(bench_handoff(steps, warmup)))
+        return
+    if args.only == "layers":
+        print(json.dumps(bench_layers(steps, warmup)))
         return
 
     want_cpu = args.only is None and not args.no_cpu
@@ -679,6 +757,7 @@ def main():
         line["qk_prep"] = bench_prep(steps, warmup)
         line["step_context"] = bench_context(steps, warmup)
         line["kv_handoff"] = bench_handoff(steps, warmup)
+        line["layers36_decode_step"] = bench_layers(steps, warmup)
     print(json.dumps(line))
 
 

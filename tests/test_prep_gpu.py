@@ -1,10 +1,14 @@
 """Fused pre-attention step (nvs_qk_norm_rope_store) on the GPU against the
-CPU oracle (oracle/prep_oracle.py, oracle/kv_oracle.py).
+CPU oracle (oracle/prep_oracle.py, oracle/kv_oracle.py) and against the
+reference's own torch ops.
 
-Bit-exact: the rotated q and k equal the oracle's (which fixes the order of
-the norm's sum, left open by the reference, to the kernel's), and the cache
-holds the rotated k and the raw v cast or quantised exactly as the store
-oracle does from those values; slots < 0 leave the cache untouched."""
+Against the oracle, bit-exact: the rotated q and k equal the oracle's (which
+fixes the order of the norm's sum, left open by the reference, to the
+kernel's), and the cache holds the rotated k and the raw v cast or quantised
+exactly as the store oracle does from those values; slots < 0 leave the
+cache untouched.  Against RMSNorm.py:11-18 and RoPE.py:5-25 run as torch ops
+on the CPU (their own summation order and division by sqrt), within 2 bf16
+steps, with at least 98% of the elements equal."""
 import numpy as np
 import pytest
 import torch
@@ -100,6 +104,34 @@ def test_prep_matches_oracle(device, kv, Hq, Hkv, T):
         worst, equal = _ulps(got, ref)
         assert worst == 0, f"{name}: {worst} bf16 steps from the oracle ({1 - equal:.2%} of elements differ)"
     _check_cache(attn, kv, slots, gk, v)
+
+
+def _torch_reference(x, w, eps, cos, sin):
+    """RMSNorm.py:11-18 then RoPE.py:5-25 as torch ops (CPU): the normed
+    value is rounded to the input dtype between the two, as there."""
+    x32 = x.float()
+    normed = (w.float() * x32 / torch.sqrt(x32.pow(2).mean(-1, keepdim=True) + eps)).to(x.dtype)
+    x1, x2 = torch.chunk(normed.float(), 2, dim=-1)
+    return torch.cat((x1 * cos - x2 * sin, x2 * cos + x1 * sin), dim=-1).to(x.dtype)
+
+
+@pytest.mark.parametrize("Hq,Hkv,T", [(32, 8, 512), (64, 8, 97)])
+def test_prep_matches_reference_torch_ops(device, Hq, Hkv, T):
+    say(f"qk_norm_rope_store vs torch ops Hq={Hq} Hkv={Hkv} T={T}")
+    NB, bs = 16, 64
+    attn = _layer(Hq, Hkv, "bf16", NB, bs, device)
+    q, k, v, qw, kw, pos, slots = _inputs(T, Hq, Hkv, 300 + T, NB, bs)
+    table = torch.from_numpy(PO.cos_sin_table(D, MAX_POS, 1e6))  # [max_pos, D]: cos | sin
+    q_rot, k_rot = attn.qk_norm_rope_store(
+        q.to(device), k.to(device), v.to(device), pos.to(device), qw.to(device), kw.to(device), 1e-6,
+        table.reshape(MAX_POS, 1, D).to(device), slots.to(device), want_k=True)
+    torch.cuda.synchronize()
+    cos, sin = table[pos].unsqueeze(1).chunk(2, dim=-1)  # [T, 1, D/2]
+    for name, got, x, w in (("q", q_rot, q, qw), ("k", k_rot, k, kw)):
+        ref = _torch_reference(x, w, 1e-6, cos, sin)
+        worst, equal = _ulps(bf16_to_np(got), bf16_to_np(ref))
+        say(f"  {name}: at most {worst} bf16 steps from the torch ops, {equal:.4%} of elements equal")
+        assert worst <= 2 and equal >= 0.98, f"{name}: {worst} bf16 steps, {equal:.2%} equal"
 
 
 def test_prep_clamps_positions_and_handles_empty_batches(device):
