@@ -7,8 +7,11 @@ fixes the order of the norm's sum, left open by the reference, to the
 kernel's), and the cache holds the rotated k and the raw v cast or quantised
 exactly as the store oracle does from those values; slots < 0 leave the
 cache untouched.  Against RMSNorm.py:11-18 and RoPE.py:5-25 run as torch ops
-on the CPU (their own summation order and division by sqrt), within 2 bf16
-steps, with at least 98% of the elements equal."""
+on the CPU (their own summation order and division by sqrt): at least 99.9%
+of the elements equal and none more than 4 bf16 steps apart.  The norm's sum
+in another order can move a normed value by one step (rounded to bf16
+between norm and rotation, as the reference does); where the rotation
+x1 cos - x2 sin cancels, that step is several steps of the smaller result."""
 import numpy as np
 import pytest
 import torch
@@ -131,7 +134,7 @@ def test_prep_matches_reference_torch_ops(device, Hq, Hkv, T):
         ref = _torch_reference(x, w, 1e-6, cos, sin)
         worst, equal = _ulps(bf16_to_np(got), bf16_to_np(ref))
         say(f"  {name}: at most {worst} bf16 steps from the torch ops, {equal:.4%} of elements equal")
-        assert worst <= 2 and equal >= 0.98, f"{name}: {worst} bf16 steps, {equal:.2%} equal"
+        assert worst <= 4 and equal >= 0.999, f"{name}: {worst} bf16 steps, {equal:.4%} equal"
 
 
 def test_prep_clamps_positions_and_handles_empty_batches(device):
