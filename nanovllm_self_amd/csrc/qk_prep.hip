@@ -63,7 +63,25 @@ struct PrepArgs {
   int64_t ko_ts, ko_hs;
 };
 
-__device__ __forceinline__ float bf16r(float x) { return bf16_bits_to_f32(f32_to_bf16_bits(x)); }
+// The 8 values rounded to bf16 in place, two per conversion; `bits` holds
+// them packed (element 2 m in the low half of word m), as a store wants them.
+__device__ __forceinline__ void round8_bf16(float (&v)[8], u32x4& bits) {
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const uint32_t w = pack_bf16x2(v[2 * m], v[2 * m + 1]);
+    bits[m] = w;
+    v[2 * m] = __uint_as_float(w << 16);
+    v[2 * m + 1] = __uint_as_float(w & 0xffff0000u);
+  }
+}
+
+__device__ __forceinline__ void unpack8_bf16(const u32x4& w, float (&x)[8]) {
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    x[2 * m] = __uint_as_float(w[m] << 16);
+    x[2 * m + 1] = __uint_as_float(w[m] & 0xffff0000u);
+  }
+}
 
 // Products and sums rounded one by one: with contraction off the compiler
 // cannot fuse x * c - y * s into a multiply-add.  (Division is correctly
@@ -75,6 +93,17 @@ __device__ __forceinline__ float mul_rn(float a, float b) {
 __device__ __forceinline__ float add_rn(float a, float b) {
 #pragma clang fp contract(off)
   return a + b;
+}
+
+// a / b correctly rounded from y = RN(1 / b), with one multiply and two
+// fused multiply-adds instead of a division per element (Markstein's
+// theorem: q0 = RN(a y) is within an ulp of a / b, r = a - b q0 is exact in
+// an FMA, and RN(q0 + r y) = RN(a / b)).  It needs b normal and finite and
+// r not to underflow, which |a| >= 2^-100 (or a = 0) ensures.
+__device__ __forceinline__ float div_by_recip(float a, float b, float y) {
+  const float q0 = mul_rn(a, y);
+  const float r = __builtin_fmaf(-b, q0, a);
+  return __builtin_fmaf(r, y, q0);
 }
 
 // Lane j ^ m of the lane's 16-lane row, for m = 1, 2, 4, 8, as DPP moves
@@ -122,96 +151,130 @@ __device__ __forceinline__ void cache_row(void* cache, float* scales, int64_t ro
   }
 }
 
+// The per-token values a section needs: the lane's cos / sign-folded sin,
+// the token's cache row and output rows.
+struct PrepToken {
+  float c[8], s[8];
+  bool ok;           // the slot is inside the cache
+  int64_t cslot;     // the slot (0 when not ok; nothing is written then)
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  uint16_t* qo;
+  uint16_t* ko;      // null: the rotated k is not returned
+};
+
+// The token's q heads (KIND 0) or its k and v heads (KIND 1), four rows a
+// pass (head g + 4 p on lane group g), the loads of kPrepUnroll rows issued
+// before any is used (KIND 1: the k and v rows of kPrepUnroll / 2 passes).
+// Rows past the heads re-read the last one and write nothing.  q and k rows:
+// RMSNorm (mean of squares over the 128 elements, division by 128 exact),
+// rounding to bf16, rotation, rounding to bf16; q goes to q_out, k to k_out
+// and the cache; v rows go to the cache as they are (cast or quantised).
+template <int KIND, int DST>
+__device__ __forceinline__ void prep_section(const PrepArgs& a, const PrepToken& tk, const uint16_t* src, int hs,
+                                             const uint16_t* vsrc, int vhs, int H, const float (&w)[8], int g,
+                                             int j) {
+  constexpr int PER = KIND == 0 ? kPrepUnroll : kPrepUnroll / 2;  // passes per round of loads
+  const int passes = (H + 3) / 4;
+  for (int p0 = 0; p0 < passes; p0 += PER) {
+    u32x4 xw[kPrepUnroll];
+#pragma unroll
+    for (int k = 0; k < kPrepUnroll; ++k) {
+      const bool isv = KIND == 1 && k >= PER;
+      const int h = min(g + 4 * (p0 + k % PER), H - 1);
+      xw[k] = *reinterpret_cast<const u32x4*>((isv ? vsrc : src) + (uint32_t)(h * (isv ? vhs : hs) + 8 * j));
+    }
+#pragma unroll
+    for (int k = 0; k < kPrepUnroll; ++k) {
+      if (p0 + k % PER >= passes) continue;
+      const int h = g + 4 * (p0 + k % PER);
+      if (h >= H) continue;
+      if (KIND == 1 && k >= PER) {  // value head: copy / cast / quantise into the cache
+        const int64_t row = tk.cslot * a.Hkv + h;
+        if constexpr (DST == NVS_DTYPE_BF16) {
+          if (tk.ok) *reinterpret_cast<u32x4*>((uint16_t*)a.vc + row * kPrepD + 8 * j) = xw[k];
+        } else {
+          float x[8];
+          unpack8_bf16(xw[k], x);
+          cache_row<DST>(a.vc, a.vs, row, x, tk.ok);
+        }
+        continue;
+      } else {
+        float x[8];
+        unpack8_bf16(xw[k], x);
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ss = add_rn(ss, mul_rn(x[i], x[i]));
+        ss = row_sum16(ss);
+        // __builtin_sqrtf is the correctly rounded square root (HIP's
+        // __fsqrt_rn is the raw v_sqrt_f32 here, off by an ulp at times).
+        const float rms = __builtin_sqrtf(add_rn(mul_rn(ss, 1.0f / kPrepD), a.eps));
+        float n[8];
+        if (rms >= 0x1p-126f && rms <= 0x1p126f) {
+          const float inv = __fdiv_rn(1.0f, rms);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) n[i] = div_by_recip(mul_rn(w[i], x[i]), rms, inv);
+        } else {  // rms 0, subnormal, huge or not finite: divide
+#pragma unroll
+          for (int i = 0; i < 8; ++i) n[i] = __fdiv_rn(mul_rn(w[i], x[i]), rms);
+        }
+        u32x4 nb;
+        round8_bf16(n, nb);
+        // Rotary pairs (e, e + 64): lanes j and j ^ 8 hold the two halves.
+        float y[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) y[i] = add_rn(mul_rn(n[i], tk.c[i]), mul_rn(row_xor<8>(n[i]), tk.s[i]));
+        u32x4 yb;
+        round8_bf16(y, yb);
+        if constexpr (KIND == 0) {
+          *reinterpret_cast<u32x4*>(tk.qo + (uint32_t)(h * (int)a.qo_hs + 8 * j)) = yb;
+        } else {
+          if (tk.ko) *reinterpret_cast<u32x4*>(tk.ko + (uint32_t)(h * (int)a.ko_hs + 8 * j)) = yb;
+          if constexpr (DST == NVS_DTYPE_BF16) {
+            if (tk.ok) *reinterpret_cast<u32x4*>((uint16_t*)a.kc + (tk.cslot * a.Hkv + h) * kPrepD + 8 * j) = yb;
+          } else {
+            cache_row<DST>(a.kc, a.ks, tk.cslot * a.Hkv + h, y, tk.ok);
+          }
+        }
+      }
+    }
+  }
+}
+
 template <int DST>
 __global__ __launch_bounds__(kPrepThreads) void qk_prep_kernel(PrepArgs a) {
   // The token is wave-uniform (through readfirstlane, so its pointers are
   // scalar); a lane adds a 32-bit offset for its head row and elements.
   const int64_t t = (int64_t)blockIdx.x * kPrepTokens + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (t >= a.T) return;  // whole waves exit together
-  const int U = a.Hq + 2 * a.Hkv;
   const int g = (threadIdx.x >> 4) & 3, j = threadIdx.x & (kRowLanes - 1);
+  PrepToken tk;
   const int64_t slot = a.slots[t];
-  const bool ok = slot >= 0 && slot < a.total_slots;
-  const int64_t cslot = ok ? slot : 0;
+  tk.ok = slot >= 0 && slot < a.total_slots;
+  tk.cslot = tk.ok ? slot : 0;
 
   // Per token: rotary cos / sin of the lane's elements and the norm weights.
   int64_t p = a.pos[t];
   p = p < 0 ? 0 : (p >= a.max_pos ? a.max_pos - 1 : p);
   const float* cs = a.cs + p * kPrepD + 8 * (j & 7);
-  float c[8], s[8], qw[8], kw[8];
-  *reinterpret_cast<f32x4*>(c) = *reinterpret_cast<const f32x4*>(cs);
-  *reinterpret_cast<f32x4*>(c + 4) = *reinterpret_cast<const f32x4*>(cs + 4);
-  *reinterpret_cast<f32x4*>(s) = *reinterpret_cast<const f32x4*>(cs + 64);
-  *reinterpret_cast<f32x4*>(s + 4) = *reinterpret_cast<const f32x4*>(cs + 68);
+  float qw[8], kw[8];
+  *reinterpret_cast<f32x4*>(tk.c) = *reinterpret_cast<const f32x4*>(cs);
+  *reinterpret_cast<f32x4*>(tk.c + 4) = *reinterpret_cast<const f32x4*>(cs + 4);
+  *reinterpret_cast<f32x4*>(tk.s) = *reinterpret_cast<const f32x4*>(cs + 64);
+  *reinterpret_cast<f32x4*>(tk.s + 4) = *reinterpret_cast<const f32x4*>(cs + 68);
   load8<NVS_DTYPE_BF16>(a.qw + 8 * j, qw);
   load8<NVS_DTYPE_BF16>(a.kw + 8 * j, kw);
+  // First half: y1 = x1 cos - x2 sin; second half: y2 = x2 cos + x1 sin.
+  // a - b and a + (-b) round identically, so both halves are one add of a
+  // product whose sine carries the sign.
   const bool first = j < 8;
-  const uint16_t* const q_tok = a.q + t * a.q_ts;
-  const uint16_t* const k_tok = a.k + t * a.k_ts;
-  const uint16_t* const v_tok = a.v + t * a.v_ts;
-  uint16_t* const qo_tok = a.qo + t * a.qo_ts;
-  uint16_t* const ko_tok = a.ko ? a.ko + t * a.ko_ts : nullptr;
-
-  const int passes = (U + 3) / 4;
-  for (int i0 = 0; i0 < passes; i0 += kPrepUnroll) {
-    float x[kPrepUnroll][8];
 #pragma unroll
-    for (int k = 0; k < kPrepUnroll; ++k) {
-      const int u = g + 4 * (i0 + k);
-      if (u >= U) continue;
-      const uint16_t* src;
-      int off;
-      if (u < a.Hq) {
-        src = q_tok;
-        off = u * (int)a.q_hs;
-      } else if (u < a.Hq + a.Hkv) {
-        src = k_tok;
-        off = (u - a.Hq) * (int)a.k_hs;
-      } else {
-        src = v_tok;
-        off = (u - a.Hq - a.Hkv) * (int)a.v_hs;
-      }
-      load8<NVS_DTYPE_BF16>(src + (uint32_t)(off + 8 * j), x[k]);
-    }
-#pragma unroll
-    for (int k = 0; k < kPrepUnroll; ++k) {
-      const int u = g + 4 * (i0 + k);
-      if (u >= U) continue;
-      if (u >= a.Hq + a.Hkv) {  // value head: cast / quantise into the cache
-        cache_row<DST>(a.vc, a.vs, cslot * a.Hkv + (u - a.Hq - a.Hkv), x[k], ok);
-        continue;
-      }
-      const bool is_q = u < a.Hq;
-      const int h = is_q ? u : u - a.Hq;
-      // RMSNorm: mean of squares over the 128 elements (division by 128 is exact).
-      float ss = 0.0f;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) ss = add_rn(ss, mul_rn(x[k][i], x[k][i]));
-      ss = row_sum16(ss);
-      // __builtin_sqrtf is the correctly rounded square root (HIP's __fsqrt_rn
-      // is the raw v_sqrt_f32 here, off by an ulp at times).
-      const float rms = __builtin_sqrtf(add_rn(mul_rn(ss, 1.0f / kPrepD), a.eps));
-      float n[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) n[i] = bf16r(__fdiv_rn(mul_rn(is_q ? qw[i] : kw[i], x[k][i]), rms));
-      // Rotary pairs (e, e + 64): lanes j and j ^ 8 hold the two halves.
-      // first half: y1 = x1 cos - x2 sin; second half: y2 = x2 cos + x1 sin.
-      // a - b and a + (-b) round identically, so both halves are one add of
-      // a product whose factor carries the sign.
-      float y[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float other = row_xor<8>(n[i]);
-        y[i] = bf16r(add_rn(mul_rn(n[i], c[i]), mul_rn(first ? -other : other, s[i])));
-      }
-      if (is_q) {
-        store8_float<NVS_DTYPE_BF16>(qo_tok + (uint32_t)(h * (int)a.qo_hs + 8 * j), y);
-        continue;
-      }
-      if (ko_tok) store8_float<NVS_DTYPE_BF16>(ko_tok + (uint32_t)(h * (int)a.ko_hs + 8 * j), y);
-      cache_row<DST>(a.kc, a.ks, cslot * a.Hkv + h, y, ok);
-    }
-  }
+  for (int i = 0; i < 8; ++i) tk.s[i] = first ? -tk.s[i] : tk.s[i];
+  tk.qo = a.qo + t * a.qo_ts;
+  tk.ko = a.ko ? a.ko + t * a.ko_ts : nullptr;
+  prep_section<0, DST>(a, tk, a.q + t * a.q_ts, (int)a.q_hs, nullptr, 0, a.Hq, qw, g, j);
+  prep_section<1, DST>(a, tk, a.k + t * a.k_ts, (int)a.k_hs, a.v + t * a.v_ts, (int)a.v_hs, a.Hkv, kw, g, j);
 }
 
 bool is_code_dtype(int dt) { return dt == NVS_DTYPE_INT8 || dt == NVS_DTYPE_FP8_E4M3; }

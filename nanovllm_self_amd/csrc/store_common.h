@@ -43,7 +43,7 @@ __device__ __forceinline__ void store8_float(void* p, const float (&x)[8]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       if constexpr (DST == NVS_DTYPE_BF16)
-        w[i] = f32_to_bf16_bits(x[2 * i]) | (f32_to_bf16_bits(x[2 * i + 1]) << 16);
+        w[i] = pack_bf16x2(x[2 * i], x[2 * i + 1]);  // one conversion per pair, the same bits
       else
         w[i] = f32_to_f16_bits(x[2 * i]) | (f32_to_f16_bits(x[2 * i + 1]) << 16);
     }
