@@ -2,8 +2,9 @@
 """Static check of the generated prefill tile loop (prefill_mx_asm.inc): every
 register an instruction writes must be a declared clobber or an output of
 the asm statement, so the compiler never keeps a value of its own in a
-register the loop overwrites.  Also checks that no instruction reads a
-scalar input it is not given.  Run by the build after the generator."""
+register the loop overwrites (exec, which the claim narrows to one lane,
+is restored by the statement itself).  Run by the build after the
+generator."""
 from __future__ import annotations
 
 import os
@@ -13,11 +14,12 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 
 # outputs of the asm statement (paged_prefill_mx.hip): O (a64-a191), l_run
-# (v218-v219), the mask limit (v220-v221, read and written)
-OUTPUTS = {f"a{i}" for i in range(64, 192)} | {"v218", "v219", "v220", "v221"}
+# (v218-v219), the mask limit (v220-v221, read and written), the claim (v243)
+OUTPUTS = {f"a{i}" for i in range(64, 192)} | {"v218", "v219", "v220", "v221", "v243"}
+RESTORED = {"exec"}
 
 NO_DEST = ("s_waitcnt", "s_nop", "s_barrier", "s_branch", "s_cbranch", "s_cmp", "s_bitcmp",
-           "buffer_load", "ds_write", "s_endpgm", "global_store", "buffer_store")
+           "ds_write", "s_endpgm", "global_store", "buffer_store")
 
 
 def regs(tok: str):
@@ -36,7 +38,8 @@ def regs(tok: str):
 
 def dests(ins: str):
     op, _, rest = ins.partition(" ")
-    if not rest or op.endswith(":") or any(op.startswith(p) for p in NO_DEST):
+    direct = op.startswith("buffer_load") and rest.rstrip().endswith(" lds")  # writes LDS only
+    if not rest or op.endswith(":") or direct or any(op.startswith(p) for p in NO_DEST):
         out = []
     else:
         first = rest.split(",")[0]
@@ -64,7 +67,7 @@ def parse_inc(path):
 
 def check(path=os.path.join(HERE, "prefill_mx_asm.inc")):
     blocks, clob = parse_inc(path)
-    allowed = clob | OUTPUTS | {"scc"}  # scc: clobbered too
+    allowed = clob | OUTPUTS | RESTORED | {"scc"}  # scc: clobbered too
     bad = []
     for name, lines in blocks.items():
         for ln in lines:

@@ -103,6 +103,9 @@ S_KROW, S_VROW, S_K, S_NT, S_JM, S_BS, S_NB, S_M0W, S_SCALE = (
 S_RBT = "s[36:39]"  # buffer resource of the sequence's block-table row (paged)
 S_RBT_NREC = "s38"  # its size in bytes: 4 x the blocks of the sequence
 S_BLK012 = ["s33", "s34", "s35"]  # block ids of tiles 0, 1, 2 (paged; from the plan)
+S_WID = "s53"        # the wave's index in the work-group
+S_CNT = "s[54:55]"   # address of the XCD's unit counter
+CLAIM = "v243"       # out: the claimed counter value (wave 0, lane 0)
 # loop state
 S_J, S_LAST = "s64", "s65"
 S_B = ["s66", "s67", "s68"]        # block ids of tiles j, j+1, j+2 (paged)
@@ -599,6 +602,23 @@ def block_mask(em, par):
             em(f"v_cndmask_b32_e64 {Sr(par, kb, qb, v)}, {Sr(par, kb, qb, v)}, {NINF}, {masks[k]}")
 
 
+def claim(em, u):
+    """Wave 0, lane 0 claims a unit for the work-group: an atomic add of 1 on
+    the XCD's counter whose old value lands in CLAIM while the loop runs (the
+    loop's last vmcnt(0) completes it; every other lane and wave gets 0)."""
+    em(f"v_mov_b32 {CLAIM}, 0")
+    em(f"s_cmp_lg_u32 {S_WID}, 0")
+    em(f"s_cbranch_scc1 {u}claimed")
+    em(f"s_mov_b64 {S_F0}, exec")
+    em("s_mov_b64 exec, 1")
+    em(f"v_mov_b32 {ET[0]}, 0")
+    em(f"v_mov_b32 {ET[1]}, 1")
+    em("s_nop 4")
+    em(f"global_atomic_add {CLAIM}, {ET[0]}, {ET[1]}, {S_CNT} sc0")
+    em(f"s_mov_b64 exec, {S_F0}")
+    em(f"{u}claimed:")
+
+
 def block_prologue(em, paged):
     """State init, block ids of tiles 0 and 1 (inputs), QK_0.  K_0 and K_1
     are in the K buffers when the loop starts (the caller copies them in
@@ -660,6 +680,7 @@ def program(paged):
     em = Emitter()
     u = "L%=_"
     mark(em, None)
+    claim(em, u)
     block_prologue(em, paged)
     # iteration 0
     em(f"s_cmp_gt_i32 {S_JM}, 0")
