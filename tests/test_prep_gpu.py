@@ -109,6 +109,46 @@ def test_prep_matches_oracle(device, kv, Hq, Hkv, T):
     _check_cache(attn, kv, slots, gk, v)
 
 
+def _edge_rows(x: torch.Tensor, g: torch.Generator) -> torch.Tensor:
+    """x [T, H, D] with rows at the edges of the norm's arithmetic: scaled by
+    2^-90 (tiny, normal quotients), 2^-80 (squares underflow to 0), 2^70
+    (squares overflow), and an all-zero row."""
+    x = x.clone().float()
+    T, H, _ = x.shape
+    cells = [(t, h) for t in range(T) for h in range(H)]
+    pick = torch.randperm(len(cells), generator=g)[:4 * max(1, len(cells) // 8)].tolist()
+    for n, i in enumerate(pick):
+        t, h = cells[i]
+        x[t, h] = x[t, h] * (2.0 ** (-90), 2.0 ** (-80), 2.0 ** 70, 0.0)[n % 4]
+    return x.to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("eps", [0.0, 1e-6])
+def test_prep_edge_rows_match_oracle(device, eps):
+    """Rows whose rms is 0 or infinite take the per-element division, tiny
+    rows the reciprocal path: both equal the oracle bit for bit (NaN where
+    the reference's arithmetic gives NaN)."""
+    say(f"qk_norm_rope_store edge rows eps={eps}")
+    Hq, Hkv, T, NB, bs = 8, 2, 16, 4, 64
+    attn = _layer(Hq, Hkv, "bf16", NB, bs, device)
+    q, k, v, qw, kw, pos, slots = _inputs(T, Hq, Hkv, 77, NB, bs)
+    g = torch.Generator().manual_seed(78)
+    q, k = _edge_rows(q, g), _edge_rows(k, g)
+    table = PO.cos_sin_table(D, MAX_POS, 1e6)
+    q_rot, k_rot = attn.qk_norm_rope_store(
+        q.to(device), k.to(device), v.to(device), pos.to(device), qw.to(device), kw.to(device), eps,
+        torch.from_numpy(table).reshape(MAX_POS, 1, D).to(device), slots.to(device), want_k=True)
+    torch.cuda.synchronize()
+    with np.errstate(all="ignore"):
+        qo, ko = PO.qk_norm_rope(bf16_to_np(q), bf16_to_np(k), pos.numpy(), bf16_to_np(qw), bf16_to_np(kw), eps,
+                                 table)
+    for name, got, ref in (("q", bf16_to_np(q_rot), qo), ("k", bf16_to_np(k_rot), ko)):
+        nan = np.isnan(ref)
+        assert np.array_equal(np.isnan(got), nan), f"{name}: NaN positions differ"
+        assert np.array_equal(got[~nan], ref[~nan]), f"{name}: differs from the oracle"
+        say(f"  {name}: {int(nan.sum())} NaN, {int(np.isinf(ref).sum())} inf elements, equal")
+
+
 def _torch_reference(x, w, eps, cos, sin):
     """RMSNorm.py:11-18 then RoPE.py:5-25 as torch ops (CPU): the normed
     value is rounded to the input dtype between the two, as there."""
