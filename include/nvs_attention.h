@@ -187,6 +187,25 @@ int64_t nvs_attention_workspace_bytes(int num_seqs, int max_seqlen_q,
                                       int block_size);
 
 /*
+ * The same with the cache dtype: for an int8 / fp8 cache and a batch with
+ * prefill rows (max_seqlen_q > 1) it adds room for a bf16 copy of the
+ * prefill rows' keys and values (min(num_seqs x ceil(max_seqlen_k / 64),
+ * 1 GiB / (64 x num_kv_heads x 128 x 4)) tiles of 64 keys), the copy the
+ * reference's prefill_torch makes per sequence before it attends
+ * (attention.py:268-273: (code.float() * scale).to(bf16)).  Given at least
+ * this much, nvs_paged_attention dequantises into the copy and runs the
+ * MFMA tile-loop prefill kernel on it; given only
+ * nvs_attention_workspace_bytes(...), or a batch whose prefill rows need
+ * more tiles, its prefill kernel dequantises inside its tile fill instead
+ * (the same values, slower).  Other dtypes: the same as
+ * nvs_attention_workspace_bytes.  num_kv_heads must be given (> 0).
+ */
+int64_t nvs_attention_workspace_bytes_cache(int num_seqs, int max_seqlen_q,
+                                            int max_seqlen_k, int num_heads,
+                                            int num_kv_heads, int head_dim,
+                                            int block_size, int cache_dtype);
+
+/*
  * Causal varlen attention over a paged KV cache: the paged call of
  * prefill_flashattn (reference attention.py:356-375,
  * flash_attn_varlen_func(..., block_table=...)) and equally the

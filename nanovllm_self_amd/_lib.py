@@ -48,6 +48,7 @@ SIGNATURES = {
         [_P, _P, _I, _P, _P, _P, _L, _I, _P, _I, _I, _L, _I, _I, _I, _P, _P, _I, _P, _P],
     ),
     "nvs_attention_workspace_bytes": (_L, [_I, _I, _I, _I, _I, _I, _I]),
+    "nvs_attention_workspace_bytes_cache": (_L, [_I, _I, _I, _I, _I, _I, _I, _I]),
     "nvs_paged_attention": (
         _I,
         [

@@ -74,6 +74,27 @@ static int launch_prefill_any(const AttnParams& P, const Plan& plan, hipStream_t
   return prefill_mx_serves(P) ? launch_prefill_mx(P, plan, s) : launch_prefill(P, plan, s);
 }
 
+// Whether a paged call over a code cache can serve its prefill rows from a
+// bf16 copy through the tile-loop kernel: the workspace holds the copy after
+// the plan and the decode partials, and both prefill kernels tile the query
+// positions alike (the plan is shared; which one runs is decided on the
+// device).  NVS_PREFILL_KERNEL=classic keeps every call on the classic
+// kernel.
+static bool shadow_serves(const AttnParams& P) {
+  if (!is_quant(P.cache_dtype) || P.max_seqlen_q <= 1 || P.bt == nullptr) return false;
+  const int g = P.Hq / P.Hkv;
+  if (prefill_mx_positions(g) != prefill_positions(g)) return false;
+  const int64_t base = align256(attention_workspace_bytes(P.B, P.max_seqlen_q, P.max_seqlen_k, P.Hq, P.Hkv));
+  if (shadow_cap(P.B, P.max_seqlen_k, P.Hkv) <= 0) return false;
+  if (P.ws_bytes < base + shadow_bytes(P.B, P.max_seqlen_k, P.Hkv)) return false;
+  // The copy is read as a bf16 cache of block size 64.
+  AttnParams C = P;
+  C.cache_dtype = NVS_DTYPE_BF16;
+  C.bs = kShadowTile;
+  C.NB = shadow_cap(P.B, P.max_seqlen_k, P.Hkv);
+  return prefill_mx_serves(C);
+}
+
 int decode_launch_waves(int max_waves, int Hkv) {
   const int w = std::min(max_waves, device_slots(4 * kDecodeWavesPerEU));
   return std::max(Hkv, w / Hkv * Hkv);
@@ -86,6 +107,18 @@ extern "C" int64_t nvs_attention_workspace_bytes(int num_seqs, int max_seqlen_q,
   (void)head_dim;
   (void)block_size;
   return attention_workspace_bytes(num_seqs, max_seqlen_q, max_seqlen_k, num_heads, num_kv_heads);
+}
+
+extern "C" int64_t nvs_attention_workspace_bytes_cache(int num_seqs, int max_seqlen_q, int max_seqlen_k,
+                                                       int num_heads, int num_kv_heads, int head_dim,
+                                                       int block_size, int cache_dtype) {
+  (void)head_dim;
+  (void)block_size;
+  const int64_t base = attention_workspace_bytes(num_seqs, max_seqlen_q, max_seqlen_k, num_heads, num_kv_heads);
+  if (base <= 0 || !is_quant(cache_dtype) || max_seqlen_q <= 1 || num_kv_heads <= 0 ||
+      num_heads % num_kv_heads != 0)
+    return base;
+  return align256(base) + shadow_bytes(num_seqs, max_seqlen_k, num_kv_heads);
 }
 
 static int check_workspace(const AttnParams& P, const char* who) {
@@ -145,14 +178,38 @@ static int paged_attention_impl(AttnParams& P, const void* q, int64_t q_tok_stri
   rc = check_workspace(P, "paged_attention");
   if (rc != NVS_OK) return rc;
   hipStream_t s = (hipStream_t)stream;
-  const Plan plan = make_plan(workspace, P);
+  const bool shadow = shadow_serves(P);
+  const Plan plan = shadow ? plan_at(workspace, P.B, prefill_tiles(P.max_seqlen_q, prefill_mx_positions(P.Hq / P.Hkv)),
+                                     prefill_mx_positions(P.Hq / P.Hkv))
+                           : make_plan(workspace, P);
   char* partials = (char*)workspace + align256(plan_bytes(num_seqs, plan.ntq));
   const int max_waves = decode_wave_cap(num_seqs, max_seqlen_k, num_kv_heads);
   rc = launch_decode(P, max_waves, decode_launch_waves(max_waves, num_kv_heads), partials, s);
   if (rc != NVS_OK || max_seqlen_q == 1) return rc;  // no prefill rows: no plan
-  rc = launch_plan(P, plan, /*paged=*/true, s);
+  if (!shadow) {
+    rc = launch_plan(P, plan, /*paged=*/true, s);
+    if (rc != NVS_OK) return rc;
+    return launch_prefill_any(P, plan, s);
+  }
+  // Code cache: the prefill rows' keys and values dequantised into the bf16
+  // copy, read by the tile-loop kernel; the classic kernel serves the call
+  // instead where the plan finds that the copy would not fit.
+  const ShadowLayout sh = shadow_at((char*)workspace + align256(attention_workspace_bytes(
+                                        P.B, P.max_seqlen_q, P.max_seqlen_k, P.Hq, P.Hkv)),
+                                    P.B, P.max_seqlen_k, P.Hkv);
+  rc = launch_plan(P, plan, /*paged=*/true, s, &sh);
   if (rc != NVS_OK) return rc;
-  return launch_prefill_any(P, plan, s);
+  rc = launch_shadow_fill(P, plan, sh, s);
+  if (rc != NVS_OK) return rc;
+  AttnParams C = P;
+  C.kc = sh.k; C.vc = sh.v; C.cache_dtype = NVS_DTYPE_BF16; C.ks = nullptr; C.vs = nullptr;
+  C.bt = sh.table; C.bt_stride = sh.ST; C.bs = kShadowTile; C.NB = sh.cap;
+  C.gate = &plan.hdr->shadow_on; C.gate_run = 1;
+  rc = launch_prefill_mx(C, plan, s);
+  if (rc != NVS_OK) return rc;
+  AttnParams F = P;
+  F.gate = &plan.hdr->shadow_on; F.gate_run = 0;
+  return launch_prefill(F, plan, s);
 }
 
 extern "C" int nvs_paged_attention(const void* q, int64_t q_tok_stride, int64_t q_head_stride,

@@ -96,7 +96,9 @@ __host__ __device__ inline int prefill_head_groups(int g) { return (g + kPrefill
 struct PlanHeader {
   int n_prefill;        // prefill list entries
   int prefill_next[8];  // per-XCD work counters of the prefill kernel (zeroed by the plan)
-  int pad[55];          // keeps the list 256-byte aligned
+  int shadow_tiles;     // code caches: 64-key tiles of the prefill rows' bf16 copy
+  int shadow_on;        // 1: the copy fits and the tile-loop kernel serves the prefill
+  int pad[53];          // keeps the list 256-byte aligned
 };
 static_assert(sizeof(PlanHeader) == 256, "plan header is one 256-byte line");
 
@@ -189,7 +191,57 @@ struct AttnParams {
   int64_t out_ts, out_hs;
   void* ws;
   int64_t ws_bytes;
+  // Prefill kernels launched side by side run only where *gate == gate_run
+  // (null: always): the plan decides on the device which one serves.
+  const int* gate;
+  int gate_run;
 };
+
+// Code caches (int8 / fp8): the prefill rows' keys and values are first
+// dequantised, bf16(code x scale) exactly as the reference's prefill_torch
+// does per sequence (attention.py:268-273), into a bf16 copy in the
+// workspace made of 64-key tiles [tile, 64, Hkv, 128], one run of tiles per
+// prefill row, with a table row per sequence mapping its 64-key tile t to a
+// copy tile; the MFMA tile-loop kernel then reads the copy as a bf16 paged
+// cache of block size 64.  The copy's capacity is the batch bound (rows x
+// ceil(max_seqlen_k / 64) tiles), at most kShadowMaxBytes; a batch whose
+// prefill rows need more tiles falls back, on the device, to the classic
+// kernel, which dequantises in its tile fill.
+constexpr int kShadowTile = 64;
+constexpr int64_t kShadowMaxBytes = 1ll << 30;  // K + V copy
+struct ShadowLayout {
+  int* base;    // [B + 1]: first copy tile of row b (exclusive prefix; base[B] = all)
+  int* table;   // [B, ST]: copy tile of row b's 64-key tile t
+  uint16_t* k;  // [cap, 64, Hkv, 128] bf16
+  uint16_t* v;
+  int ST;       // table row length: ceil(max_seqlen_k / 64)
+  int cap;      // copy tiles
+};
+inline int64_t shadow_tile_bytes(int Hkv) { return (int64_t)kShadowTile * Hkv * kHeadDim * 2; }
+inline int shadow_cap(int B, int max_seqlen_k, int Hkv) {
+  const int64_t st = ((int64_t)max_seqlen_k + kShadowTile - 1) / kShadowTile;
+  const int64_t most = kShadowMaxBytes / (2 * shadow_tile_bytes(Hkv > 0 ? Hkv : 1));
+  const int64_t c = (int64_t)B * st < most ? (int64_t)B * st : most;
+  return (int)(c > 0 ? c : 0);
+}
+inline int64_t shadow_bytes(int B, int max_seqlen_k, int Hkv) {
+  const int64_t st = ((int64_t)max_seqlen_k + kShadowTile - 1) / kShadowTile;
+  return align256((int64_t)(B + 1) * 4) + align256((int64_t)B * st * 4) +
+         2 * (int64_t)shadow_cap(B, max_seqlen_k, Hkv) * shadow_tile_bytes(Hkv);
+}
+inline ShadowLayout shadow_at(void* p, int B, int max_seqlen_k, int Hkv) {
+  ShadowLayout s;
+  s.ST = (int)(((int64_t)max_seqlen_k + kShadowTile - 1) / kShadowTile);
+  s.cap = shadow_cap(B, max_seqlen_k, Hkv);
+  char* c = (char*)p;
+  s.base = (int*)c;
+  c += align256((int64_t)(B + 1) * 4);
+  s.table = (int*)c;
+  c += align256((int64_t)B * s.ST * 4);
+  s.k = (uint16_t*)c;
+  s.v = (uint16_t*)(c + (int64_t)s.cap * shadow_tile_bytes(Hkv));
+  return s;
+}
 
 int64_t decode_workspace_bytes(int max_waves, int group);
 int64_t attention_workspace_bytes(int num_seqs, int max_seqlen_q, int max_seqlen_k, int num_heads,
@@ -198,7 +250,11 @@ int64_t attention_workspace_bytes(int num_seqs, int max_seqlen_q, int max_seqlen
 // bound (max_waves) and the device's resident wave slots, whichever is
 // smaller.
 int decode_launch_waves(int max_waves, int Hkv);
-int launch_plan(const AttnParams& P, const Plan& plan, bool paged, hipStream_t stream);
+int launch_plan(const AttnParams& P, const Plan& plan, bool paged, hipStream_t stream,
+                const ShadowLayout* shadow = nullptr);
+// Dequantises the prefill rows' tiles into the copy (runs only where the
+// plan set shadow_on).
+int launch_shadow_fill(const AttnParams& P, const Plan& plan, const ShadowLayout& sh, hipStream_t stream);
 int launch_decode(const AttnParams& P, int max_waves, int waves, void* partials, hipStream_t stream);
 int launch_prefill(const AttnParams& P, const Plan& plan, hipStream_t stream);
 // The MFMA tile-loop prefill kernel (paged_prefill_mx.hip): whether it serves

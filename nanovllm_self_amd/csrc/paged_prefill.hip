@@ -71,6 +71,8 @@ struct PrefillArgs {
   float scale_log2;
   uint16_t* out;
   int64_t out_ts, out_hs;
+  const int* gate;  // run only where *gate == gate_run (null: always)
+  int gate_run;
 };
 
 // 16-byte chunk swizzle of key row `key`: a bijection of key % 16 that maps
@@ -456,6 +458,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(PrefillArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t lds[2 * 2 * kTile];  // Kbuf[2], Vbuf[2]
   __shared__ int blk_lds[kBlockWindow];
   __shared__ int s_claim[2];
+  if (a.gate && *a.gate != a.gate_run) return;  // the other prefill kernel serves this call
   const int per_entry = a.Hkv * a.hgroups;
   const int units = a.plan.hdr->n_prefill * per_entry;
   const int xcd = blockIdx.x & 7;
@@ -496,6 +499,7 @@ int launch_prefill(const AttnParams& P, const Plan& plan, hipStream_t stream) {
   a.plan = plan;
   a.scale_log2 = P.softmax_scale * 1.4426950408889634f;
   a.out = (uint16_t*)P.out; a.out_ts = P.out_ts; a.out_hs = P.out_hs;
+  a.gate = P.gate; a.gate_run = P.gate_run;
   if (plan.ntq <= 0 || P.B <= 0) return NVS_OK;
   if (plan.pbm != kRows * a.nblk) {
     set_error("prefill: plan tile of %d positions does not match %d heads per kv head", plan.pbm, a.g);

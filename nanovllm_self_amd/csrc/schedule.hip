@@ -16,7 +16,15 @@ struct PlanArgs {
   int64_t NB;
   int bs;
   Plan plan;
+  int* shadow_base;  // code caches: per-row first tile of the bf16 copy (null: no copy)
+  int shadow_cap;
+  int shadow_st;     // tiles of a table row: a row's tiles past it are not copied
 };
+
+// Tiles of the bf16 copy for a prefill row with kl keys.
+__device__ __forceinline__ int shadow_row_tiles(const PlanArgs& a, int np, int kl) {
+  return np > 0 && kl > 0 ? min((kl + kShadowTile - 1) / kShadowTile, a.shadow_st) : 0;
+}
 
 // Block id of the tile of keys [64 t, 64 t + 64) of row b: -1 past the
 // row's blocks or outside the pool.
@@ -82,6 +90,31 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanArgs a) {
   // the causal mask).  Row-major order keeps the work-groups of an XCD on the
   // same sequence at the same time, so the K/V tiles they all read come
   // from HBM once and from L2 after that.
+  // ---- code caches: the prefill rows' 64-key tiles of the bf16 copy, row
+  // by row (an exclusive scan of ceil(k_len / 64)); the copy serves the call
+  // if they fit.
+  bool shadow = false;
+  if (a.shadow_base) {
+    int sbase = 0;
+    for (int b0 = 0; b0 < a.B; b0 += kPlanThreads) {
+      bool dec;
+      int np, q0, kl, tot;
+      row_work(a, b0 + tid, dec, np, q0, kl);
+      const int nt = shadow_row_tiles(a, np, kl);
+      const int incl = block_scan_1024(nt, scan_lds, tot);
+      if (b0 + tid < a.B) a.shadow_base[b0 + tid] = sbase + incl - nt;
+      sbase += tot;
+    }
+    shadow = sbase <= a.shadow_cap;
+    if (tid == 0) {
+      a.shadow_base[a.B] = sbase;
+      pl.hdr->shadow_tiles = sbase;
+      pl.hdr->shadow_on = shadow ? 1 : 0;
+    }
+  } else if (tid == 0) {
+    pl.hdr->shadow_tiles = 0;
+    pl.hdr->shadow_on = 0;
+  }
   int base = 0;
   for (int b0 = 0; b0 < a.B; b0 += kPlanThreads) {
     bool dec;
@@ -95,9 +128,16 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanArgs a) {
       r.L = a.cu_q[b + 1] - q0;
       r.k0 = k0;
       r.K = kl;
-      r.blk0 = a.paged ? tile_block(a, b, kl, 0) : -1;
-      r.blk1 = a.paged ? tile_block(a, b, kl, 1) : -1;
-      r.blk2 = a.paged ? tile_block(a, b, kl, 2) : -1;
+      if (shadow) {  // tiles of the copy (the thread wrote shadow_base[b] itself)
+        const int sb = a.shadow_base[b], nt = shadow_row_tiles(a, np, kl);
+        r.blk0 = 0 < nt ? sb : -1;
+        r.blk1 = 1 < nt ? sb + 1 : -1;
+        r.blk2 = 2 < nt ? sb + 2 : -1;
+      } else {
+        r.blk0 = a.paged ? tile_block(a, b, kl, 0) : -1;
+        r.blk1 = a.paged ? tile_block(a, b, kl, 1) : -1;
+        r.blk2 = a.paged ? tile_block(a, b, kl, 2) : -1;
+      }
       for (int i = 0; i < np; ++i) {
         const int e = base + incl - np + i;
         r.item = b * pl.ntq + (np - 1 - i);
@@ -124,7 +164,7 @@ int device_slots(int per_cu) {
   return g_cus[dev] * per_cu;
 }
 
-int launch_plan(const AttnParams& P, const Plan& plan, bool paged, hipStream_t stream) {
+int launch_plan(const AttnParams& P, const Plan& plan, bool paged, hipStream_t stream, const ShadowLayout* shadow) {
   PlanArgs a;
   a.cu_q = P.cu_q;
   a.cu_k = P.cu_k;
@@ -136,6 +176,9 @@ int launch_plan(const AttnParams& P, const Plan& plan, bool paged, hipStream_t s
   a.NB = P.NB;
   a.bs = P.bs > 0 ? P.bs : 64;
   a.plan = plan;
+  a.shadow_base = shadow ? shadow->base : nullptr;
+  a.shadow_cap = shadow ? shadow->cap : 0;
+  a.shadow_st = shadow ? shadow->ST : 0;
   hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(1024), 0, stream, a);
   return check_launch("plan");
 }

@@ -285,8 +285,16 @@ class PagedAttention(nn.Module):
         lib = _lib.load()
         stream = _lib.stream_of(q)
         max_q, max_k = int(context.max_seqlen_q), int(context.max_seqlen_k)
-        ws_bytes = int(lib.nvs_attention_workspace_bytes(
-            B, max_q, max_k, self.num_heads, self.num_kv_heads, self.head_dim, 0))
+        if (context.block_tables is not None and self.k_cache is not None
+                and self.k_cache.dtype in (torch.int8, torch.float8_e4m3fn)):
+            # int8 / fp8 caches: room for the bf16 copy of the prefill rows'
+            # keys and values that the tile-loop prefill kernel reads.
+            ws_bytes = int(lib.nvs_attention_workspace_bytes_cache(
+                B, max_q, max_k, self.num_heads, self.num_kv_heads, self.head_dim, 0,
+                _lib.nvs_dtype(self.k_cache.dtype)))
+        else:
+            ws_bytes = int(lib.nvs_attention_workspace_bytes(
+                B, max_q, max_k, self.num_heads, self.num_kv_heads, self.head_dim, 0))
         ws = attention_workspace(q.device, ws_bytes)
         if context.block_tables is None:
             k = k.to(compute) if k.dtype != compute else k
