@@ -225,6 +225,22 @@ def bench_prefill(steps, warmup, cpu=False):
         log("cpu baseline: prefill_8b")
         res["cpu_baseline"] = cpu_prefill_leg(wl, 10.0, "prefill_8b")
     del wl
+    torch.cuda.empty_cache()
+    # The same batch over an fp8 cache: the prefill rows' keys and values are
+    # dequantised into a bf16 copy and the tile-loop kernel runs on it.
+    log("building prefill_8b (fp8 cache)")
+    wl = W.prefill_8b("cuda", kv="fp8")
+    ms_step8, _ = timed_steps(step(wl), steps, warmup)
+    _, ms_attn8 = timed_steps(attention_only(wl), steps, warmup)
+    res["fp8_cache"] = {
+        "ms_per_step": ms_step8,
+        "ms_attention": ms_attn8,
+        "tflops": flops / ms_attn8 / 1e9,
+        "vs_bf16_cache": ms_attn / ms_attn8,
+    }
+    log(f"prefill_8b/fp8 cache: attention {ms_attn8:.3f} ms -> {res['fp8_cache']['tflops']:.0f} TFLOP/s")
+    del wl
+    torch.cuda.empty_cache()
     return res
 
 

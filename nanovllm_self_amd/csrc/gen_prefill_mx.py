@@ -346,12 +346,13 @@ V_FIRST = True  # issue segment A's first V reads before the fills' set-up
 NA = 12  # exponential pairs of segment A
 
 
-def read_ahead_a(em, ppar, spar, i):
+def read_ahead_a(em, ppar, spar, i, last=False):
     """Segment A's read-ahead after PV operand i: V operand i + AHEAD, or,
-    in the last AHEAD slots, the first K operands of segment B."""
+    in the last AHEAD slots, the first K operands of segment B (none in a
+    unit's last iteration, whose segment B has no QK^T)."""
     if i + AHEAD < 16:
         v_read(em, ppar, i + AHEAD)
-    else:
+    elif not last:
         k_read(em, spar, i + AHEAD - 16)
 
 # Optional callback mark(em, k) at the phase boundaries of an iteration
@@ -450,13 +451,14 @@ def take_block_id(em, dst):
 
 
 # ----------------------------------------------------------------- blocks
-def block_iteration(em, paged, par, first, lbl):
+def block_iteration(em, paged, par, first, lbl, last=False):
     """Iteration j (parity par): fill K_{j+2}, V_j (spread over segment A);
     segment A (PV_{j-1} unless first) beside the max / m update and the
     first exponentials; segment B (QK_{j+1}) beside the rest; the row-sum
     check; barrier.  Paged: the block id of tile j+2 (loaded an iteration
     earlier; iteration 0: from the plan) is taken first and the load of
-    tile j+3's issued."""
+    tile j+3's issued.  The unit's last iteration (last) has no tile j+1:
+    no K fill, no K reads and segment B is its VALU work alone."""
     ppar, spar = 1 - par, 1 - par
     if V_FIRST and not first:
         for i in range(AHEAD):
@@ -475,7 +477,7 @@ def block_iteration(em, paged, par, first, lbl):
         em(f"s_lshl_b32 {S_ROW[2]}, {S_T[2]}, 6")
     em(f"s_add_u32 {S_T[2]}, {S_J}, 2")
     mark(em, 0)
-    fill = fill_tile(paged, "k", S_ROW[2], S_T[2], S_B[2] if paged else None, par)
+    fill = [] if last else fill_tile(paged, "k", S_ROW[2], S_T[2], S_B[2] if paged else None, par)
     fill += fill_tile(paged, "v", S_ROW[0], S_J, S_B[0] if paged else None, par)
     # ---- segment A
     pairs = exp_pairs(par)
@@ -507,16 +509,16 @@ def block_iteration(em, paged, par, first, lbl):
             mf = pv_mfmas(em, i, ppar)
             em(mf[0])
             if READ_EARLY:
-                read_ahead_a(em, ppar, spar, i)
+                read_ahead_a(em, ppar, spar, i, last)
             emit_items(em, slots[2 * i])
             em(mf[1])
             emit_items(em, slots[2 * i + 1])
             if not READ_EARLY:
-                read_ahead_a(em, ppar, spar, i)
+                read_ahead_a(em, ppar, spar, i, last)
         mark(em, 1)
     # ---- segment B
     slots = spread(b_items, 32)
-    for i in range(16):
+    for i in range(0 if last else 16):
         em.lds_wait(("k", i))
         mf = qk_mfmas(i, spar)
         em(mf[0])
@@ -527,6 +529,8 @@ def block_iteration(em, paged, par, first, lbl):
         emit_items(em, slots[2 * i + 1])
         if not READ_EARLY and i + AHEAD < 16:
             k_read(em, spar, i + AHEAD)
+    if last:
+        emit_items(em, b_items)
     # The tile's row sums, taken with the running max of the tiles before:
     # past SUM_LIMIT or not finite (a max that was stale or still -inf) on
     # any lane, the slow path redoes the tile with its own max.
@@ -626,8 +630,6 @@ def block_prologue(em, paged):
     caller's prefetch of the next unit's query rows may still be in flight,
     and the first wait on vmcnt is the one that ends iteration 0."""
     em("s_nop 1")
-    for i in range(128):
-        em(f"v_accvgpr_write_b32 a{64 + i}, 0")
     em(f"v_mov_b32 {MRUN[0]}, 0xff800000")
     em(f"v_mov_b32 {MRUN[1]}, 0xff800000")
     em(f"v_mov_b32 {LRUN[0]}, 0")
@@ -648,12 +650,17 @@ def block_prologue(em, paged):
         em(f"s_mov_b32 {S_ROW[1]}, 64")
     for i in range(AHEAD):
         k_read(em, 0, i)
+    # O^T <- 0 (128 AGPRs), four writes beside each QK_0 MFMA
+    zero = [f"v_accvgpr_write_b32 a{64 + r}, 0" for r in range(128)]
     for i in range(16):
         em.lds_wait(("k", i))
         for x in qk_mfmas(i, 0):
             em(x)
+            for _ in range(4):
+                em(zero.pop(0))
         if i + AHEAD < 16:
             k_read(em, 0, i + AHEAD)
+    assert not zero
     # every wave has read K_0 before iteration 0 refills its buffer
     em("s_waitcnt lgkmcnt(0)")
     em.lds = []
@@ -698,14 +705,23 @@ def program(paged):
         em(f"s_cbranch_scc1 {u}nomask{par}")
         block_mask(em, par)
         em(f"{u}nomask{par}:")
+        em(f"s_cmp_eq_u32 {S_J}, {S_LAST}")
+        em(f"s_cbranch_scc1 {u}last{par}")
         block_iteration(em, paged, par, False, f"{u}f{par}")
         em.lds = []
         em(f"s_add_u32 {S_J}, {S_J}, 1")
     em(f"s_branch {u}top")
+    # the unit's last iteration (j = S_LAST >= 1), out of line
+    for par in (1, 0):
+        em(f"{u}last{par}:")
+        block_iteration(em, paged, par, False, f"{u}l{par}", last=True)
+        em.lds = []
+        em(f"s_branch {u}final")
     # out-of-line slow paths
     block_slow(em, 0, f"{u}i0")
     for par in (1, 0):
         block_slow(em, par, f"{u}f{par}")
+        block_slow(em, par, f"{u}l{par}")
     em(f"{u}final:")
     em("s_waitcnt vmcnt(0) lgkmcnt(0)")  # no load may land after the asm
     em.lds = []
