@@ -110,3 +110,14 @@ def test_copy_over_capacity_falls_back_on_the_device(device):
     ids = [0, 35, 71]
     _, hdr = _run_checked(wl, ids, "copy over capacity")
     assert hdr[HDR_SHADOW_TILES] == 72 * 63 and hdr[HDR_SHADOW_ON] == 0
+
+
+@pytest.mark.parametrize("g", [1, 2, 5, 8])
+def test_copy_path_gqa_groups(device, g):
+    """Group sizes whose query tiling the two prefill kernels share (1, 2, 8:
+    the copy) and one they do not (5: the classic kernel's fill), fp8."""
+    say(f"code-cache prefill g={g}")
+    spec = [(256, 129), (0, 63), (512, 200), (0, 1)]
+    wl = _batch(spec, 2 * g, 2, "fp8", seed=70 + g)
+    _, hdr = _run_checked(wl, list(range(len(spec))), f"code-cache prefill g={g}")
+    assert hdr[HDR_SHADOW_ON] == (0 if g == 5 else 1)
