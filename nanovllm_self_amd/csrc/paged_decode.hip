@@ -125,6 +125,19 @@ __device__ __forceinline__ LaneOffsets lane_offsets(int Hkv, int col, int grp) {
   return o;
 }
 
+// The cache's K / V bytes are read once per call: loads marked
+// non-temporal (`nt`) keep them from displacing other lines in the caches on
+// their way.  Measured on decode_8b: 252 -> 228 us per call; on the
+// decode_quant batch bf16 471 -> 429, fp8 256 -> 239, int8 266 -> 251 us.
+#ifndef NVS_DECODE_NT
+#define NVS_DECODE_NT 1
+#endif
+template <typename T>
+__device__ __forceinline__ T kv_load(const T* p) {
+  if constexpr (NVS_DECODE_NT) return __builtin_nontemporal_load(p);
+  else return *p;
+}
+
 // Loads of one 32-key tile of kv head h whose first key sits at offset koff
 // of pool block blk (-1: missing; the loads then read block 0, in bounds).
 // Every address is a wave-uniform row base plus a 32-bit lane offset.
@@ -142,22 +155,25 @@ __device__ __forceinline__ void decode_load(DecodeTile<KV>& T, const DecodeArgs&
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int s = 0; s < 4; ++s) T.k[t][s] = *reinterpret_cast<const u32x4*>(kb + 16 * t * rowb + 64 * s + ok);
+      for (int s = 0; s < 4; ++s) T.k[t][s] = kv_load(reinterpret_cast<const u32x4*>(kb + 16 * t * rowb + 64 * s + ok));
 #pragma unroll
-    for (int e = 0; e < 8; ++e) T.v[e] = *reinterpret_cast<const u32x4*>(vb + slot_key(e, 0) * rowb + ov);
+    for (int e = 0; e < 8; ++e) T.v[e] = kv_load(reinterpret_cast<const u32x4*>(vb + slot_key(e, 0) * rowb + ov));
   } else {
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      T.k[t][0] = *reinterpret_cast<const u32x4*>(kb + 16 * t * rowb + ok);
-      T.k[t][1] = *reinterpret_cast<const u32x4*>(kb + 16 * t * rowb + 16 + ok);
+      T.k[t][0] = kv_load(reinterpret_cast<const u32x4*>(kb + 16 * t * rowb + ok));
+      T.k[t][1] = kv_load(reinterpret_cast<const u32x4*>(kb + 16 * t * rowb + 16 + ok));
     }
 #pragma unroll
-    for (int e = 0; e < 8; ++e) T.v[e] = *reinterpret_cast<const u32x2*>(vb + slot_key(e, 0) * rowb + ov);
+    for (int e = 0; e < 8; ++e) T.v[e] = kv_load(reinterpret_cast<const u32x2*>(vb + slot_key(e, 0) * rowb + ov));
     // One scale per lane (lanes 0-31 the k scales of the tile's keys, 32-63
     // the v scales); the compute hands each lane its keys' scales with
     // cross-lane reads.
     const uint32_t so = lane_off((uint32_t)(threadIdx.x & 31) * (uint32_t)a.Hkv * 4u);
     const char* sb = (const char*)(((threadIdx.x < 32) ? a.ks : a.vs) + row0);
+    // A plain load: 4-byte scales of rows Hkv x 4 bytes apart, marked
+    // non-temporal, made the fp8 decode_quant call 5 % slower (251 against
+    // 239 us).
     T.sc = *reinterpret_cast<const float*>(sb + so);
   }
 }

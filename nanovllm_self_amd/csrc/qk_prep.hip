@@ -131,6 +131,26 @@ __device__ __forceinline__ float row_sum16(float v) {
   return add_rn(v, row_xor<8>(v));
 }
 
+// Every source row is read once and every destination row written once:
+// both marked non-temporal (`nt`), which keeps the stream from displacing
+// other lines in the caches (36 864 tokens: 180 -> 165 us; the loads alone
+// marked: 186 us, the stores alone: 174 us).
+#ifndef NVS_PREP_NT
+#define NVS_PREP_NT 1
+#endif
+#ifndef NVS_PREP_NTS
+#define NVS_PREP_NTS 1
+#endif
+__device__ __forceinline__ u32x4 prep_load(const u32x4* p) {
+  if constexpr (NVS_PREP_NT) return __builtin_nontemporal_load(p);
+  else return *p;
+}
+template <typename V>
+__device__ __forceinline__ void prep_store(V* p, V v) {
+  if constexpr (NVS_PREP_NTS) __builtin_nontemporal_store(v, p);
+  else *p = v;
+}
+
 // Writes lane j's 8 elements of head row `row` of a cache of dtype DST;
 // quantised caches take the row scale from the absmax over the row's lanes.
 template <int DST>
@@ -142,7 +162,7 @@ __device__ __forceinline__ void cache_row(void* cache, float* scales, int64_t ro
     constexpr float qmax = (DST == NVS_DTYPE_INT8) ? QuantInt8::kQmax : QuantFp8::kQmax;
     const float sc = quant_scale(row_absmax(x, kRowLanes), qmax);
     if (write) {
-      *reinterpret_cast<u32x2*>((uint8_t*)cache + e) = quant8<DST>(x, sc);
+      prep_store(reinterpret_cast<u32x2*>((uint8_t*)cache + e), quant8<DST>(x, sc));
       if (j == 0) scales[row] = sc;
     }
   } else {
@@ -183,7 +203,7 @@ __device__ __forceinline__ void prep_section(const PrepArgs& a, const PrepToken&
     for (int k = 0; k < kPrepUnroll; ++k) {
       const bool isv = KIND == 1 && k >= PER;
       const int h = min(g + 4 * (p0 + k % PER), H - 1);
-      xw[k] = *reinterpret_cast<const u32x4*>((isv ? vsrc : src) + (uint32_t)(h * (isv ? vhs : hs) + 8 * j));
+      xw[k] = prep_load(reinterpret_cast<const u32x4*>((isv ? vsrc : src) + (uint32_t)(h * (isv ? vhs : hs) + 8 * j)));
     }
 #pragma unroll
     for (int k = 0; k < kPrepUnroll; ++k) {
@@ -193,7 +213,7 @@ __device__ __forceinline__ void prep_section(const PrepArgs& a, const PrepToken&
       if (KIND == 1 && k >= PER) {  // value head: copy / cast / quantise into the cache
         const int64_t row = tk.cslot * a.Hkv + h;
         if constexpr (DST == NVS_DTYPE_BF16) {
-          if (tk.ok) *reinterpret_cast<u32x4*>((uint16_t*)a.vc + row * kPrepD + 8 * j) = xw[k];
+          if (tk.ok) prep_store(reinterpret_cast<u32x4*>((uint16_t*)a.vc + row * kPrepD + 8 * j), xw[k]);
         } else {
           float x[8];
           unpack8_bf16(xw[k], x);
@@ -228,11 +248,11 @@ __device__ __forceinline__ void prep_section(const PrepArgs& a, const PrepToken&
         u32x4 yb;
         round8_bf16(y, yb);
         if constexpr (KIND == 0) {
-          *reinterpret_cast<u32x4*>(tk.qo + (uint32_t)(h * (int)a.qo_hs + 8 * j)) = yb;
+          prep_store(reinterpret_cast<u32x4*>(tk.qo + (uint32_t)(h * (int)a.qo_hs + 8 * j)), yb);
         } else {
-          if (tk.ko) *reinterpret_cast<u32x4*>(tk.ko + (uint32_t)(h * (int)a.ko_hs + 8 * j)) = yb;
+          if (tk.ko) prep_store(reinterpret_cast<u32x4*>(tk.ko + (uint32_t)(h * (int)a.ko_hs + 8 * j)), yb);
           if constexpr (DST == NVS_DTYPE_BF16) {
-            if (tk.ok) *reinterpret_cast<u32x4*>((uint16_t*)a.kc + (tk.cslot * a.Hkv + h) * kPrepD + 8 * j) = yb;
+            if (tk.ok) prep_store(reinterpret_cast<u32x4*>((uint16_t*)a.kc + (tk.cslot * a.Hkv + h) * kPrepD + 8 * j), yb);
           } else {
             cache_row<DST>(a.kc, a.ks, tk.cslot * a.Hkv + h, y, tk.ok);
           }
