@@ -263,14 +263,18 @@ class PagedAttention(nn.Module):
         store_slots the same call first writes k / v to those cache slots
         (nvs_paged_attention_store, paged mode only)."""
         compute = torch.bfloat16
-        # The reference also computes in fp16 (attention_compute_dtype float16,
-        # attention.py:22-23, 327-330); these kernels compute in bf16 only, so
-        # fp16 is refused in both modes rather than rounded to bf16.
-        if self.attention_compute_dtype == torch.float16 or q.dtype == torch.float16 or (
-                context.block_tables is None and (k.dtype == torch.float16 or v.dtype == torch.float16)):
+        # These kernels compute in bf16, the reference's default
+        # attention_compute_dtype (config.py:33-38).  A layer set to compute
+        # in another dtype (fp16: attention.py:22-23, 327-330; fp32 through
+        # the eager path) is refused in both modes rather than computed in
+        # bf16.  q / k / v of another dtype are cast to the compute dtype, as
+        # the reference casts them (attention.py:340-342, 362).
+        if self.attention_compute_dtype != compute:
+            name = {torch.float16: "fp16", torch.float32: "fp32"}.get(self.attention_compute_dtype,
+                                                                      str(self.attention_compute_dtype))
             raise RuntimeError(
-                "HIP attention computes in bf16: fp16 attention (attention_compute_dtype float16 or fp16 "
-                "q/k/v) is not served")
+                f"HIP attention computes in bf16: {name} attention (attention_compute_dtype "
+                f"{self.attention_compute_dtype}) is not served")
         if q.dtype != compute:
             q = q.to(compute)
         _need_device(q, "q")

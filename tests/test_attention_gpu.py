@@ -194,6 +194,25 @@ def test_local_mode_strided_views(device):
     compare(bf16_to_np(out), ref.numpy(), False, "local strided")
 
 
+@pytest.mark.parametrize("paged", [False, True])
+def test_fp16_inputs_are_cast_to_the_compute_dtype(device, paged):
+    """fp16 q / k / v (an fp16 model) with bf16 compute: cast to bf16 before
+    the attention, as the reference's q.to(attention_compute_dtype) does
+    (attention.py:340-342, 362); the result equals the call on the cast
+    inputs bit for bit."""
+    say(f"fp16 inputs, bf16 compute, paged={paged}")
+    spec = [(256, 100), (0, 37), (512, 1)] if paged else [(0, 100), (0, 37), (0, 1)]
+    tabs = _tables([p + n for p, n in spec], 12, 17)
+    wl = _custom([SeqSlice(tabs[i], p, n) for i, (p, n) in enumerate(spec)], 8, 2, 12, seed=17)
+    assert (wl.context.block_tables is not None) == paged
+    q16, k16, v16 = (t.to(torch.float16) for t in (wl.q, wl.k, wl.v))
+    out16 = wl.attn.forward(q16, k16, v16, wl.context)
+    ref = wl.attn.forward(q16.to(torch.bfloat16), k16.to(torch.bfloat16), v16.to(torch.bfloat16), wl.context)
+    torch.cuda.synchronize()
+    assert out16.dtype == torch.bfloat16
+    assert torch.equal(out16, ref)
+
+
 def test_prefix_equals_fresh(device):
     """A sequence run as cached prefix + chunk gives the rows a fresh prefill
     of the whole sequence gives."""

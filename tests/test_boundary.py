@@ -174,6 +174,24 @@ def test_fp16_attention_is_refused_in_both_modes(paged):
         a.prefill_flashattn(z, z, z, ctx)
 
 
+@pytest.mark.parametrize("paged", [False, True])
+def test_fp32_attention_is_refused_in_both_modes(paged):
+    """fp32 compute (the reference's eager path allows it) is not served
+    either: the layer raises instead of computing in bf16."""
+    a = PagedAttention(8, 8, 128)
+    a.block_size = 256
+    a.k_cache = torch.zeros(1, 256, 8, 128, dtype=torch.bfloat16)
+    a.v_cache = torch.zeros_like(a.k_cache)
+    a.kv_cache_dtype = torch.bfloat16
+    a.attention_compute_dtype = torch.float32
+    z = torch.zeros(1, 8, 128, dtype=torch.float32)
+    cu = torch.tensor([0, 1], dtype=torch.int32)
+    ctx = Context(cu_seqlens_q=cu, cu_seqlens_k=cu, max_seqlen_q=1, max_seqlen_k=1,
+                  block_tables=torch.zeros(1, 1, dtype=torch.int32) if paged else None)
+    with pytest.raises(RuntimeError, match="fp32 attention"):
+        a.prefill_torch(z, z, z, ctx)
+
+
 def test_no_cpu_fallback():
     a = PagedAttention(8, 8, 128)
     a.block_size = 256
