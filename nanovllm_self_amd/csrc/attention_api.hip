@@ -207,6 +207,9 @@ static int paged_attention_impl(AttnParams& P, const void* q, int64_t q_tok_stri
   C.gate = &plan.hdr->shadow_on; C.gate_run = 1;
   rc = launch_prefill_mx(C, plan, s);
   if (rc != NVS_OK) return rc;
+  // When every row's tiles fit the copy whatever the lengths, the plan
+  // cannot turn the copy off and the classic kernel would only exit.
+  if ((int64_t)sh.cap >= (int64_t)P.B * sh.ST) return NVS_OK;
   AttnParams F = P;
   F.gate = &plan.hdr->shadow_on; F.gate_run = 0;
   return launch_prefill(F, plan, s);
