@@ -125,15 +125,19 @@ __device__ __forceinline__ LaneOffsets lane_offsets(int Hkv, int col, int grp) {
   return o;
 }
 
-// The cache's K / V bytes are read once per call: loads marked
-// non-temporal (`nt`) keep them from displacing other lines in the caches on
-// their way.  Measured on decode_8b: 252 -> 228 us per call; on the
-// decode_quant batch bf16 471 -> 429, fp8 256 -> 239, int8 266 -> 251 us.
+// The cache's V bytes are read once per call, each load instruction taking
+// whole 128-byte lines: those loads are marked non-temporal (`nt`), which
+// keeps the stream from displacing other lines in the caches on its way
+// (decode_8b: 252 -> 228 us per call; decode_quant bf16 471 -> 429, fp8
+// 256 -> 240 us).  A K load instruction takes half of each line it touches
+// (16 key rows x 64 bytes), the other half coming with the next instruction:
+// K stays a plain load, since an `nt` line can leave the cache in between
+// (K marked `nt` as well: fp8 233 -> 240 us, bf16 428 -> 429 us).
 #ifndef NVS_DECODE_NT
 #define NVS_DECODE_NT 1
 #endif
 template <typename T>
-__device__ __forceinline__ T kv_load(const T* p) {
+__device__ __forceinline__ T v_load(const T* p) {
   if constexpr (NVS_DECODE_NT) return __builtin_nontemporal_load(p);
   else return *p;
 }
@@ -155,17 +159,17 @@ __device__ __forceinline__ void decode_load(DecodeTile<KV>& T, const DecodeArgs&
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int s = 0; s < 4; ++s) T.k[t][s] = kv_load(reinterpret_cast<const u32x4*>(kb + 16 * t * rowb + 64 * s + ok));
+      for (int s = 0; s < 4; ++s) T.k[t][s] = *reinterpret_cast<const u32x4*>(kb + 16 * t * rowb + 64 * s + ok);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) T.v[e] = kv_load(reinterpret_cast<const u32x4*>(vb + slot_key(e, 0) * rowb + ov));
+    for (int e = 0; e < 8; ++e) T.v[e] = v_load(reinterpret_cast<const u32x4*>(vb + slot_key(e, 0) * rowb + ov));
   } else {
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      T.k[t][0] = kv_load(reinterpret_cast<const u32x4*>(kb + 16 * t * rowb + ok));
-      T.k[t][1] = kv_load(reinterpret_cast<const u32x4*>(kb + 16 * t * rowb + 16 + ok));
+      T.k[t][0] = *reinterpret_cast<const u32x4*>(kb + 16 * t * rowb + ok);
+      T.k[t][1] = *reinterpret_cast<const u32x4*>(kb + 16 * t * rowb + 16 + ok);
     }
 #pragma unroll
-    for (int e = 0; e < 8; ++e) T.v[e] = kv_load(reinterpret_cast<const u32x2*>(vb + slot_key(e, 0) * rowb + ov));
+    for (int e = 0; e < 8; ++e) T.v[e] = v_load(reinterpret_cast<const u32x2*>(vb + slot_key(e, 0) * rowb + ov));
     // One scale per lane (lanes 0-31 the k scales of the tile's keys, 32-63
     // the v scales); the compute hands each lane its keys' scales with
     // cross-lane reads.
