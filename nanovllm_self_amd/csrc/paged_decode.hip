@@ -837,11 +837,13 @@ void paged_decode_kernel(DecodeArgs a, const int32_t* __restrict__ bt, const int
   // all of them here, before the ring's state exists, so the walk's
   // registers are free again by the main loop; then the rows no owner
   // writes, by every wave.  The wave's own load of a row's last tile must
-  // follow the row's write: a workgroup-scope release fence (a wait for the
-  // wave's own stores, no cache maintenance) goes before the first loads if
-  // a row ends in the tiles they cover or the wave wrote a row no owner
-  // writes, otherwise just before the load of the first written row's last
-  // tile (fence_tile), so the writes overlap the stream.
+  // follow the row's write in the wave's program order (one wave's vector
+  // memory operations reach its CU's L1 in issue order): a workgroup-scope
+  // release fence, which keeps the compiler from moving the load above the
+  // write and, with one wave per work-group, adds no wait, goes before the
+  // first loads if a row ends in the tiles they cover or the wave wrote a
+  // row no owner writes, otherwise just before the load of the first
+  // written row's last tile (fence_tile).
   int fence_tile = INT_MAX;
   if (a.kn) {
     Cursor c = n[0];
