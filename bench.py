@@ -496,6 +496,22 @@ def bench_mixed(steps, warmup, cpu=False):
                        "step's decode bytes / prefill FLOPs", **cpu_host())
         del wl
         torch.cuda.empty_cache()
+        if kv == "bf16":
+            # The step's four prefill chunks alone (2048 rows over 0-16 K
+            # cached keys each): the prefill kernel's rate on long units.
+            log("building mixed_32b prefill chunks (bf16)")
+            wc = W.mixed_32b_chunks("cuda", kv=kv)
+            pf_c = wc.prefill_flops()
+            _, ms_c = timed_steps(attention_only(wc), steps, warmup)
+            out[kv]["prefill_chunks"] = {
+                "flops": pf_c,
+                "ms_attention": ms_c,
+                "tflops": pf_c / ms_c / 1e9,
+                "frac_bf16_peak": pf_c / ms_c / 1e9 / BF16_PEAK_TFLOPS,
+            }
+            log(f"mixed_32b prefill chunks alone: attention {ms_c:.3f} ms -> {pf_c / ms_c / 1e9:.0f} TFLOP/s")
+            del wc
+            torch.cuda.empty_cache()
     return out
 
 

@@ -222,6 +222,14 @@ def mixed_32b(device="cuda", kv="bf16", n_decode=128, n_chunks=4, chunk=2048) ->
     return _assemble("mixed_32b", seqs, 64, 8, 128, 256, 16384, kv, device, g, seed=4)
 
 
+def mixed_32b_chunks(device="cuda", kv="bf16") -> Workload:
+    """mixed_32b's four prefill chunks alone: the same draw (tables, prefixes,
+    cache contents of those sequences) without the decode rows."""
+    g = _gen(4)
+    seqs = _mixed_32b_seqs(g, 128, 4, 2048)[128:]
+    return _assemble("mixed_32b chunks", seqs, 64, 8, 128, 256, 16384, kv, device, g, seed=4)
+
+
 def step_batches() -> dict:
     """The sequence lists (block size 256) of decode_8b, prefill_8b,
     decode_quant and mixed_32b, drawn as their builders draw them, without

@@ -7,7 +7,8 @@ bottom-right mask), so the CPU cost is the block's, not the sequence's.
 Covered: the longest prefill_8b sequence (its first query tile, tiles
 across the middle, its last, partial tile); mixed_32b's chunk over the
 longest cached prefix and its longest and shortest decode rows, bf16 and
-fp8; the same shape with a chunk over 16384 cached tokens and decode rows
+fp8; its four chunks alone (the prefill batch bench.py times on long
+units); the same shape with a chunk over 16384 cached tokens and decode rows
 of 24K-32K keys; a block_size-64 prefill past 32768 keys, where the prefill kernel
 reloads the block-table window it stages in LDS (512 entries).  Bars as in
 gpu_util: bf16 max-abs 2e-2 / mean-abs 2e-3, quantised max-abs 5e-2 (reference
@@ -66,6 +67,25 @@ def test_mixed_32b_longest_chunk(mixed):
     L = wl.seqs[i].num_new_tokens
     _check_blocks(wl, got, i, [(0, 64), (1000, 1064), (L - 64, L)],
                   f"mixed_32b/{wl.kv} chunk {i} (P={wl.seqs[i].num_cached_tokens})")
+
+
+def test_mixed_32b_chunks_alone(device):
+    """The batch bench.py times for the prefill kernel on long units:
+    mixed_32b's four chunks without the decode rows (no q_len == 1 row: the
+    decode launch finds no tile).  The same prefixes and tables as in the
+    full draw; row blocks of every chunk against the oracle."""
+    say("mixed_32b prefill chunks alone (bf16)")
+    wl = W.mixed_32b_chunks(device)
+    full = W._mixed_32b_seqs(W._gen(4), 128, 4, 2048)[128:]
+    assert [(s.num_cached_tokens, s.num_new_tokens) for s in wl.seqs] == \
+        [(s.num_cached_tokens, s.num_new_tokens) for s in full]
+    assert all(s.num_new_tokens == 2048 for s in wl.seqs)
+    got = _run(wl)
+    for i, s in enumerate(wl.seqs):
+        _check_blocks(wl, got, i, [(0, 32), (2048 - 64, 2048)],
+                      f"mixed_32b chunk {i} alone (P={s.num_cached_tokens})")
+    del wl
+    torch.cuda.empty_cache()
 
 
 def test_mixed_32b_extreme_decode_rows(mixed):
