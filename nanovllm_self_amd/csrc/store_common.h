@@ -54,6 +54,29 @@ __device__ __forceinline__ void store8_float(void* p, const float (&x)[8]) {
 // Quantise a row chunk (8 values) given the row scale; 8 one-byte codes.
 template <int DST>
 __device__ __forceinline__ u32x2 quant8(const float (&x)[8], float scale) {
+  if constexpr (DST == NVS_DTYPE_FP8_E4M3) {
+    // A finite scale means a finite row, so every clamped quotient is a
+    // finite value in [-448, 448]: gfx950's conversion (OCP e4m3, round to
+    // nearest even, two values per instruction) encodes it as f32_to_e4m3
+    // does, without that encoder's per-value branches.  Rows holding inf or
+    // NaN (scale inf or NaN) take the bit-level encoder below.
+    if (__builtin_isfinite(scale)) {
+      float y[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float v = x[i] / scale;
+        y[i] = v < -448.0f ? -448.0f : (v > 448.0f ? 448.0f : v);
+      }
+      u32x2 w;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        int c = __builtin_amdgcn_cvt_pk_fp8_f32(y[4 * h], y[4 * h + 1], 0, false);
+        c = __builtin_amdgcn_cvt_pk_fp8_f32(y[4 * h + 2], y[4 * h + 3], c, true);
+        w[h] = (uint32_t)c;
+      }
+      return w;
+    }
+  }
   u32x2 w = {0u, 0u};
 #pragma unroll
   for (int i = 0; i < 8; ++i) {

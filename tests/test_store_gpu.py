@@ -151,6 +151,48 @@ def test_fp8_hardware_decode_matches_ocp_e4m3(device):
     assert np.array_equal(out[~nan], ref[~nan])
 
 
+def _e4m3_probe_values() -> np.ndarray:
+    """Every finite bf16 value in [-448, 448]; every midpoint between
+    neighbouring e4m3 values (a tie: round to even), the f32 values on
+    either side of it, and the same around 0 and the subnormal codes; f32
+    subnormals and signed zeros."""
+    bf = (np.arange(0x10000, dtype=np.uint32) << 16).view(np.float32)
+    bf = bf[np.isfinite(bf) & (np.abs(bf) <= 448.0)]
+    pos = np.unique(KO.e4m3_decode(np.arange(0x7F, dtype=np.uint8)))  # 0 .. 448
+    mid = ((pos[:-1].astype(np.float64) + pos[1:]) / 2).astype(np.float32)
+    near = np.concatenate([mid, np.nextafter(mid, np.float32(0)), np.nextafter(mid, np.float32(1e9)),
+                           np.float32([2.0 ** -10, 2.0 ** -11, 3 * 2.0 ** -11, 1e-40, 1.4e-45, 0.0])])
+    near = near[near <= 448.0]
+    return np.concatenate([bf, near, -near]).astype(np.float32)
+
+
+def test_fp8_encode_every_value(device):
+    """The fp8 store's encoder on every value that decides a code: rows of
+    128 whose first element is 448 have scale 448 / 448 = 1 exactly, so each
+    other element's code is its own e4m3 rounding; the codes equal the
+    oracle's round-to-nearest-even encoder (pinned against torch's cast)."""
+    say("fp8 encode every value")
+    vals = _e4m3_probe_values()
+    per = 127
+    n = (vals.size + per - 1) // per
+    rows = np.zeros((n, 128), dtype=np.float32)
+    rows[:, 0] = 448.0
+    flat = np.zeros(n * per, dtype=np.float32)
+    flat[:vals.size] = vals
+    rows[:, 1:] = flat.reshape(n, per)
+    x = torch.from_numpy(rows).reshape(n, 1, 128)
+    a = PagedAttention(1, 1, 128)
+    q, s = a.quantize_fp8_per_token(x.to(device))
+    assert np.all(s.cpu().numpy() == 1.0)
+    rq, rs = KO.quantize_fp8_per_token(rows.reshape(n, 1, 128))
+    assert np.all(rs == 1.0)
+    got = q.cpu().view(torch.uint8).numpy().reshape(n, 128)
+    want = rq.view(np.uint8).reshape(n, 128)
+    bad = np.argwhere(got != want)
+    assert bad.size == 0, (f"{len(bad)} codes differ, e.g. value {rows[tuple(bad[0])]!r}: "
+                           f"got {got[tuple(bad[0])]:#04x}, want {want[tuple(bad[0])]:#04x}")
+
+
 @pytest.mark.parametrize("kind", ["int8", "fp8"])
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_quantize_dequantize_entry_points(device, kind, out_dtype):
