@@ -89,10 +89,10 @@ __global__ __launch_bounds__(256) void store_kv_kernel(StoreArgs a) {
     float sv = 0.0f;
     if constexpr (HAS_V) sv = quant_scale(row_absmax(xv, lpr), qmax);
     if (valid) {
-      *reinterpret_cast<u32x2*>((uint8_t*)a.kc + dst_elem) = quant8<DST>(xk, sk);
+      *reinterpret_cast<u32x2*>((uint8_t*)a.kc + dst_elem) = quant8<DST, SRC != NVS_DTYPE_FP32>(xk, sk);
       if (c == 0) a.ks[dst_row] = sk;
       if constexpr (HAS_V) {
-        *reinterpret_cast<u32x2*>((uint8_t*)a.vc + dst_elem) = quant8<DST>(xv, sv);
+        *reinterpret_cast<u32x2*>((uint8_t*)a.vc + dst_elem) = quant8<DST, SRC != NVS_DTYPE_FP32>(xv, sv);
         if (c == 0) a.vs[dst_row] = sv;
       }
     }

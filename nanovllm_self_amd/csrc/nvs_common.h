@@ -122,17 +122,13 @@ __device__ __forceinline__ float quant_scale(float absmax, float qmax) {
   return (s < 1e-6f) ? 1e-6f : s;
 }
 
-__device__ __forceinline__ uint32_t quant_int8(float x, float scale) {
-  float q = __builtin_rintf(x / scale);
+// int8 code of a quotient x / scale: round half to even, clamp to +-127.
+__device__ __forceinline__ uint32_t int8_code(float quotient) {
+  float q = __builtin_rintf(quotient);
   q = q < -127.0f ? -127.0f : (q > 127.0f ? 127.0f : q);
   return ((uint32_t)(int32_t)q) & 0xffu;
 }
 
-__device__ __forceinline__ uint32_t quant_fp8(float x, float scale) {
-  float y = x / scale;
-  y = y < -448.0f ? -448.0f : (y > 448.0f ? 448.0f : y);
-  return f32_to_e4m3(y);
-}
 
 // e4m3 code (low byte) -> fp32, exact.  gfx950 converts OCP e4m3 in hardware.
 __device__ __forceinline__ float e4m3_to_f32(uint32_t code) {

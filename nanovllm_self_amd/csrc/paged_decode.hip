@@ -490,7 +490,7 @@ __device__ __forceinline__ void store_new_token(const DecodeArgs& a, int q0, int
     constexpr float qmax = (KV == NVS_DTYPE_INT8) ? QuantInt8::kQmax : QuantFp8::kQmax;
     const float sc = quant_scale(row_absmax(x, kHeadDim / 8), qmax);
     char* dst = (char*)(isv ? a.vc : a.kc) + row * (int64_t)kHeadDim;
-    *reinterpret_cast<u32x2*>(dst + 8 * c) = quant8<KV>(x, sc);
+    *reinterpret_cast<u32x2*>(dst + 8 * c) = quant8<KV, true>(x, sc);
     if (c == 0) const_cast<float*>(isv ? a.vs : a.ks)[row] = sc;
   }
 }

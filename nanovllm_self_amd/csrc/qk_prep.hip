@@ -162,7 +162,7 @@ __device__ __forceinline__ void cache_row(void* cache, float* scales, int64_t ro
     constexpr float qmax = (DST == NVS_DTYPE_INT8) ? QuantInt8::kQmax : QuantFp8::kQmax;
     const float sc = quant_scale(row_absmax(x, kRowLanes), qmax);
     if (write) {
-      prep_store(reinterpret_cast<u32x2*>((uint8_t*)cache + e), quant8<DST>(x, sc));
+      prep_store(reinterpret_cast<u32x2*>((uint8_t*)cache + e), quant8<DST, true>(x, sc));
       if (j == 0) scales[row] = sc;
     }
   } else {

@@ -51,38 +51,62 @@ __device__ __forceinline__ void store8_float(void* p, const float (&x)[8]) {
   }
 }
 
+// The quotients x[i] / scale that decide the codes.  With SRC16 (every x[i]
+// a bf16 or fp16 value, the row's scale max(absmax / qmax, 1e-6) finite)
+// they come from one reciprocal and an FMA correction,
+//   q0 = x r,  q = q0 + (x - q0 scale) r   (r = 1 / scale, q = q0 for x = 0),
+// whose int8 and e4m3 codes equal those of the correctly rounded x / scale
+// for every pair of bf16 values and every pair of fp16 values with |x| <=
+// absmax, for both qmax (checked exhaustively on gfx950; where the
+// quotients differ, as for some subnormal x, the codes do not).  fp32
+// sources, and rows with inf or NaN, take an IEEE divide per value.
+template <bool SRC16>
+__device__ __forceinline__ void quotients8(const float (&x)[8], float scale, float (&q)[8]) {
+  if (SRC16 && __builtin_isfinite(scale)) {
+    const float r = 1.0f / scale;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float q0 = x[i] * r;
+      q[i] = q0 == 0.0f ? q0 : __builtin_fmaf(__builtin_fmaf(-q0, scale, x[i]), r, q0);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) q[i] = x[i] / scale;
+  }
+}
+
 // Quantise a row chunk (8 values) given the row scale; 8 one-byte codes.
-template <int DST>
+// SRC16: the values are bf16 / fp16 ones (see quotients8).
+template <int DST, bool SRC16 = false>
 __device__ __forceinline__ u32x2 quant8(const float (&x)[8], float scale) {
+  float q[8];
+  quotients8<SRC16>(x, scale, q);
+  u32x2 w = {0u, 0u};
   if constexpr (DST == NVS_DTYPE_FP8_E4M3) {
     // A finite scale means a finite row, so every clamped quotient is a
     // finite value in [-448, 448]: gfx950's conversion (OCP e4m3, round to
     // nearest even, two values per instruction) encodes it as f32_to_e4m3
     // does, without that encoder's per-value branches.  Rows holding inf or
-    // NaN (scale inf or NaN) take the bit-level encoder below.
+    // NaN (scale inf or NaN) take the bit-level encoder.
     if (__builtin_isfinite(scale)) {
-      float y[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float v = x[i] / scale;
-        y[i] = v < -448.0f ? -448.0f : (v > 448.0f ? 448.0f : v);
-      }
-      u32x2 w;
+      for (int i = 0; i < 8; ++i) q[i] = q[i] < -448.0f ? -448.0f : (q[i] > 448.0f ? 448.0f : q[i]);
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        int c = __builtin_amdgcn_cvt_pk_fp8_f32(y[4 * h], y[4 * h + 1], 0, false);
-        c = __builtin_amdgcn_cvt_pk_fp8_f32(y[4 * h + 2], y[4 * h + 3], c, true);
+        int c = __builtin_amdgcn_cvt_pk_fp8_f32(q[4 * h], q[4 * h + 1], 0, false);
+        c = __builtin_amdgcn_cvt_pk_fp8_f32(q[4 * h + 2], q[4 * h + 3], c, true);
         w[h] = (uint32_t)c;
       }
       return w;
     }
-  }
-  u32x2 w = {0u, 0u};
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    uint32_t c = (DST == NVS_DTYPE_INT8) ? quant_int8(x[i], scale)
-                                         : quant_fp8(x[i], scale);
-    w[i >> 2] |= c << (8 * (i & 3));
+    for (int i = 0; i < 8; ++i) {
+      const float y = q[i] < -448.0f ? -448.0f : (q[i] > 448.0f ? 448.0f : q[i]);
+      w[i >> 2] |= f32_to_e4m3(y) << (8 * (i & 3));
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) w[i >> 2] |= int8_code(q[i]) << (8 * (i & 3));
   }
   return w;
 }

@@ -83,11 +83,32 @@ def test_store_cast_bit_exact(device, src, dst):
     assert np.array_equal(_f32(a.v_cache), ref_v)
 
 
-def _store_quant_case(device, mode, T=513, H=8, D=128, NB=8, bs=256, strided=False, seed=0):
+def _wide_src(shape, dtype, seed):
+    """Random finite values of the source dtype from its bit patterns: every
+    exponent, subnormals and signed zeros included; each (token, head) row
+    scaled by its own power of two so that row absmaxes span the range."""
+    g = torch.Generator().manual_seed(seed)
+    if dtype == torch.float32:
+        bits = torch.randint(-(1 << 31), 1 << 31, shape, generator=g, dtype=torch.int64).to(torch.int32)
+        x = bits.view(torch.float32).clone()
+    else:
+        bits = torch.randint(0, 1 << 16, shape, generator=g, dtype=torch.int32).to(torch.int16)
+        x = bits.view(dtype).float()
+    x = torch.where(torch.isfinite(x), x, torch.zeros_like(x))
+    lim = 6.0e4 if dtype == torch.float16 else 3.0e38
+    x = x.clamp(-lim, lim)
+    lo = -20 if dtype == torch.float16 else -40
+    shift = torch.randint(lo, 1, shape[:-1] + (1,), generator=g).float()
+    return (x * torch.exp2(shift)).to(dtype)
+
+
+def _store_quant_case(device, mode, T=513, H=8, D=128, NB=8, bs=256, strided=False, seed=0,
+                      src=torch.bfloat16, wide=False):
     cache_dtype = torch.int8 if mode == "int8_mock" else torch.float8_e4m3fn
     a = _layer(H, D, NB, bs, cache_dtype, mode, device)
-    k = _src((T, H, D), torch.bfloat16, seed + 1)
-    v = _src((T, H, D), torch.bfloat16, seed + 2)
+    make = (lambda sh, sd: _wide_src(sh, src, sd)) if wide else (lambda sh, sd: _src(sh, src, sd))
+    k = make((T, H, D), seed + 1)
+    v = make((T, H, D), seed + 2)
     k[3] = 0  # all-zero rows -> scale 1e-6, codes 0
     v[5, 2] = torch.tensor([127.0, 2.5, -2.5, 3.5] + [0.0] * (D - 4))  # exact ties
     slots = torch.randperm(NB * bs, generator=torch.Generator().manual_seed(seed + 3))[:T].to(torch.int32)
@@ -121,6 +142,17 @@ def _store_quant_case(device, mode, T=513, H=8, D=128, NB=8, bs=256, strided=Fal
 def test_store_quant_bit_exact(device, mode):
     say(f"store quant {mode}")
     _store_quant_case(device, mode)
+
+
+@pytest.mark.parametrize("src", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("mode", ["int8_mock", "fp8_e4m3"])
+def test_store_quant_wide_exponents(device, mode, src):
+    """Rows of random bit patterns (every exponent, subnormals, signed
+    zeros) at row scales from 2^-40 (fp16: 2^-20) up: the bf16 / fp16 sources take the
+    reciprocal-and-correction quotient, fp32 sources the divide; the codes
+    and scales are bit-exact against the oracle either way."""
+    say(f"store quant wide exponents {mode} {src}")
+    _store_quant_case(device, mode, T=1024, src=src, wide=True, seed=90)
 
 
 @pytest.mark.parametrize("mode", ["int8_mock", "fp8_e4m3"])
