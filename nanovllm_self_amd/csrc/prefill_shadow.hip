@@ -7,11 +7,12 @@
 // (code.float() * scale.float()).to(bf16), per token and kv head, with
 // missing blocks read as zeros (the eager gather pads them with zeros).
 //
-// Work: copy tile s (64 consecutive keys of one prefill row, every kv head,
-// K and V) per work-group iteration; the plan kernel numbered the tiles row
-// by row (ShadowLayout::base).  A work-group finds the row of its tile by a
-// binary search over those numbers, writes the table entry, and converts the
-// tile's 64 x Hkv token rows of K and of V: 16 lanes to a row (8 codes, one
+// Work: tile s (64 consecutive keys of one prefill row, every kv head, K and
+// V), or half of it when the copy has fewer tiles than work-groups, per
+// work-group iteration; the plan kernel numbered the tiles row by row
+// (ShadowLayout::base).  A work-group finds the row of its tile by a binary
+// search over those numbers, writes the table entry (first half), and
+// converts its token rows of K and of V: 16 lanes to a row (8 codes, one
 // 8-byte load, a 16-byte store each), 16 rows per pass of 256 threads.
 // Keys past the row's length are not written (the prefill kernel never
 // reads them).
@@ -64,7 +65,13 @@ __global__ __launch_bounds__(kShadowThreads) void shadow_fill_kernel(ShadowArgs 
   const int total = a.hdr->shadow_tiles;
   const int j = threadIdx.x & 15;
   const int rows = kShadowTile * a.Hkv;  // token rows of a tile (token-major, then kv head)
-  for (int s = blockIdx.x; s < total; s += gridDim.x) {
+  // A copy whose half tiles (32 keys x Hkv token rows) all fit one pass of
+  // the grid is cut into them, so that it spreads over twice as many
+  // work-groups (mixed_32b's 504 tiles: 45.7 -> 38.3 us); a larger one keeps
+  // whole tiles (prefill_8b's 833 tiles as half tiles: 49.3 -> 53.5 us).
+  const int split = 2 * total <= (int)gridDim.x ? 2 : 1;
+  for (int u = blockIdx.x; u < split * total; u += gridDim.x) {
+    const int s = split == 2 ? u >> 1 : u, half = split == 2 ? u & 1 : 0;
     // Row b of tile s: base[b] <= s < base[b + 1] (base is non-decreasing
     // with base[B] = total > s, so the largest such b has tiles).
     int lo = 0, hi = a.B;
@@ -74,7 +81,7 @@ __global__ __launch_bounds__(kShadowThreads) void shadow_fill_kernel(ShadowArgs 
     }
     const int b = lo;
     const int t = s - a.sh.base[b];  // < ST: the plan keeps a row's tiles within its table row
-    if (threadIdx.x == 0) a.sh.table[(int64_t)b * a.sh.ST + t] = s;
+    if (threadIdx.x == 0 && half == 0) a.sh.table[(int64_t)b * a.sh.ST + t] = s;
     const int K = a.cu_k[b + 1] - a.cu_k[b];
     // The tile's keys lie in one block (block_size is a multiple of 64).
     const int lb = kShadowTile * t / a.bs;
@@ -84,7 +91,9 @@ __global__ __launch_bounds__(kShadowThreads) void shadow_fill_kernel(ShadowArgs 
     const int64_t row0 = blk >= 0 ? ((int64_t)blk * a.bs + (kShadowTile * t) % a.bs) * a.Hkv : 0;
     const int keys = min(K - kShadowTile * t, kShadowTile);
     const int64_t out0 = (int64_t)s * rows;
-    for (int r = threadIdx.x >> 4; r < keys * a.Hkv; r += kShadowThreads / 16) {
+    const int span = kShadowTile / split;  // keys of the work item
+    const int r_end = min(keys, span * (half + 1)) * a.Hkv;
+    for (int r = span * half * a.Hkv + (threadIdx.x >> 4); r < r_end; r += kShadowThreads / 16) {
       u32x4 ko = {0u, 0u, 0u, 0u}, vo = {0u, 0u, 0u, 0u};
       if (blk >= 0) {
         const int64_t cr = row0 + r;  // cache row (token, kv head)
@@ -117,8 +126,8 @@ int launch_shadow_fill(const AttnParams& P, const Plan& plan, const ShadowLayout
   a.hdr = plan.hdr;
   a.sh = sh;
   if (P.B <= 0 || sh.cap <= 0) return NVS_OK;
-  // Persistent: a few work-groups per CU, never more than the copy's tiles.
-  const int wgs = (int)std::min<int64_t>((int64_t)sh.cap, (int64_t)device_slots(4));
+  // Persistent: a few work-groups per CU, never more than the copy's half tiles.
+  const int wgs = (int)std::min<int64_t>(2 * (int64_t)sh.cap, (int64_t)device_slots(4));
   dim3 grid((unsigned)std::max(1, wgs)), block(kShadowThreads);
   switch (P.cache_dtype) {
     case NVS_DTYPE_INT8:
