@@ -67,9 +67,13 @@ int nvs_version(void);
  *   k, v          [num_tokens, num_kv_heads, head_dim] of src_dtype
  *                 (BF16 / FP16 / FP32), strides (tok, head) in elements.
  *   slot_mapping  [num_tokens] int32; block = slot / block_size, offset =
- *                 slot % block_size.  Slots < 0 are skipped (padding rows);
- *                 slots >= num_blocks * block_size are skipped as well, so
- *                 the kernel never writes outside the cache.
+ *                 slot % block_size.  Precondition (what the engine's
+ *                 prepare_model_input builds, model_runner.py:461-532):
+ *                 every slot >= 0.  Outside it, slots < 0 are skipped (the
+ *                 reference's slot // bs, slot % bs would wrap -1 to the
+ *                 last row of the last block, attention.py:158-159); slots
+ *                 >= num_blocks * block_size are skipped as well, so the
+ *                 kernel never writes outside the cache.
  *   cache_dtype   BF16 / FP16 / FP32: the row is cast to the cache dtype with
  *                 round-to-nearest-even (the reference's k.to(cache_dtype)).
  *                 INT8: absmax = max|x| over head_dim in fp32,
@@ -154,7 +158,8 @@ int nvs_dequantize_per_token(const void* codes, int code_dtype,
  * Paged gather of the visible K/V of a batch, the eager path's
  * PagedAttention.get_kv_cache (reference attention.py:201-285).
  * For sequence i the non-negative entries of block_tables[i] are taken in
- * order (entries < 0 are dropped, as row[row != -1] does), flattened to
+ * order (entries < 0 are dropped; the reference's row[row != -1] drops only
+ * -1, and would index other negative ids from the end of the pool), flattened to
  * tokens and truncated to context_lens[i]; codes are dequantised to out_dtype
  * when cache_dtype is INT8 / FP8_E4M3, otherwise cast.  Positions past the
  * gathered length are zero and kv_mask (uint8, [num_seqs, max_len]) is 1
@@ -216,8 +221,13 @@ int64_t nvs_attention_workspace_bytes_cache(int num_seqs, int max_seqlen_q,
  *   cu_seqlens_k  [num_seqs + 1] int32 prefix sums of the visible KV lengths
  *                 (cached prefix + new tokens, already written to the cache).
  *   block_tables  [num_seqs, bt_stride] int32; logical block j of sequence i
- *                 is block_tables[i * bt_stride + j]; entries < 0 read as
- *                 all-zero K and V (the eager path's zero padding).
+ *                 is block_tables[i * bt_stride + j].  Precondition (what
+ *                 prepare_block_tables builds, model_runner.py:334-344):
+ *                 -1 entries only after the last block that k_len keys
+ *                 need.  Outside it, an entry < 0 inside k_len reads as
+ *                 all-zero K and V at its logical positions, where the
+ *                 reference's gather compacts (row[row != -1] drops a -1
+ *                 and shifts later keys left, attention.py:255-275).
  *   Mask: query row r of a sequence with q_len new and k_len visible tokens
  *   attends keys j <= r + (k_len - q_len) (bottom-right causal); rows with no
  *   visible key produce 0.  GQA: query head hq reads kv head

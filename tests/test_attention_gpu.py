@@ -106,7 +106,11 @@ def test_decode_gqa_groups(device, g):
 
 @pytest.mark.parametrize("kv", ["bf16", "fp8"])
 def test_decode_missing_blocks_read_as_zero(device, kv):
-    """Entries < 0 inside k_len behave like the eager path's zero padding."""
+    """An entry < 0 inside k_len (outside the engine's precondition: -1 only
+    after a row's last needed block) reads as zero K/V at its logical
+    positions.  This pins the kernels' own convention against a hand-built
+    zero-padded reference; the reference's gather would compact the row
+    instead (tests/test_oracle.py::test_gather_hole_compacts_like_reference)."""
     say(f"decode missing block {kv}")
     tabs = _tables([600, 300], 8, 5)
     wl = _custom([SeqSlice(tabs[0], 599, 1), SeqSlice(tabs[1], 299, 1)], 8, 2, 8, kv=kv, seed=5)

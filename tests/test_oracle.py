@@ -163,6 +163,29 @@ def test_gather_compacts_truncates_pads():
     assert np.array_equal(vb, -kb)
 
 
+def test_gather_hole_compacts_like_reference():
+    """A -1 inside a row's k_len (input the engine never builds: it pads -1
+    only at the tail, model_runner.py:334-344).  The reference's gather keeps
+    row[row != -1] (attention.py:255-275), so the keys of later blocks move
+    left into the hole; the HIP kernels instead read the hole as zero K/V at
+    its logical positions.  Both conventions, side by side."""
+    bs, h, d = 2, 1, 1
+    vals = np.arange(1, 11, dtype=np.float32).reshape(5, bs, h, d)  # block b holds 2b+1, 2b+2
+    bt = np.array([[2, -1, 4, 0]])  # hole at logical block 1
+    kb, _, mask = KO.get_kv_cache(vals, vals, bt, [5])
+    assert list(kb[0, :, 0, 0]) == [5, 6, 9, 10, 1]  # blocks 2, 4, 0: compacted
+    assert mask.tolist() == [[True] * 5]
+    # the kernels' convention for the same row: logical block j at keys 2j, 2j+1
+    zero_read = [5, 6, 0, 0, 9]
+    assert list(kb[0, :, 0, 0]) != zero_read
+    # torch's semantics the reference relies on: row[row != -1] drops only -1,
+    # and a negative slot wraps (slot // bs, slot % bs: -1 -> last row of block -1)
+    row = torch.tensor([2, -1, 4, -2])
+    assert row[row != -1].tolist() == [2, 4, -2]
+    slot = torch.tensor([-1])
+    assert (slot // 256).item() == -1 and (slot % 256).item() == 255
+
+
 # ----------------------------------------------------------------- attention
 def _brute(q, k, v, cu_q, cu_k, Hq, Hkv):
     """float64 loops straight from the definition."""
