@@ -13,10 +13,18 @@ import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 
-# outputs of the asm statement (paged_prefill_mx.hip): O (a64-a191), l_run
-# (v218-v219), the mask limit (v220-v221, read and written), the claim (v243)
-OUTPUTS = {f"a{i}" for i in range(64, 192)} | {"v218", "v219", "v220", "v221", "v243"}
 RESTORED = {"exec"}
+
+
+def outputs(hip=os.path.join(HERE, "paged_prefill_mx.hip")):
+    """Registers bound to outputs ("={...}") or read-write operands ("+{...}")
+    of the asm statement, read from its operand list in the kernel source."""
+    text = open(hip).read()
+    out = set()
+    for spec in re.findall(r'"[=+]\{([^}]+)\}"', text):
+        out.update(regs(spec))
+    return out
+
 
 NO_DEST = ("s_waitcnt", "s_nop", "s_barrier", "s_branch", "s_cbranch", "s_cmp", "s_bitcmp",
            "ds_write", "s_endpgm", "global_store", "buffer_store")
@@ -67,7 +75,7 @@ def parse_inc(path):
 
 def check(path=os.path.join(HERE, "prefill_mx_asm.inc")):
     blocks, clob = parse_inc(path)
-    allowed = clob | OUTPUTS | RESTORED | {"scc"}  # scc: clobbered too
+    allowed = clob | outputs() | RESTORED | {"scc"}  # scc: clobbered too
     bad = []
     for name, lines in blocks.items():
         for ln in lines:

@@ -27,10 +27,15 @@ Register map (fixed; the C++ side binds inputs and outputs to it):
   v216-217 m_run, v218-219 l_run (out), v220-221 mask limit (in/out)
   v222 -inf, v223 bf16 (1, 1), v224-231 softmax temporaries,
   v232-239 exponential temporaries, v240 block id
+  v244-v248   output descriptor (in), v[0:31] output temporaries
   a[0:63]     Q^T operands: Q[qb][st] = a[32 qb + 4 st ..]   (in)
-  a[64:191]   O^T accumulators: O[n][qb] = a[64 + 16 (2 n + qb) ..] (out)
+  a[64:191]   O^T accumulators: O[n][qb] = a[64 + 16 (2 n + qb) ..]
   a[192:223]  V operand ring (8 slots), a[224:255] K operand ring (8 slots)
-  s[40:52]    scalar inputs, s[64:101] loop state
+  s[33:63]    scalar inputs, s[64:99] loop state
+After the loop the statement copies the next unit's key tiles 0 and 1 into
+the K buffers (both free then), runs the last PV, normalises O and stores it
+as bf16 rows straight from registers: v_permlane32_swap_b32 pairs the two
+lane halves' 8-byte pieces into 16-byte chunks of one row each.
 """
 from __future__ import annotations
 
@@ -106,6 +111,13 @@ S_BLK012 = ["s33", "s34", "s35"]  # block ids of tiles 0, 1, 2 (paged; from the 
 S_WID = "s53"        # the wave's index in the work-group
 S_CNT = "s[54:55]"   # address of the XCD's unit counter
 CLAIM = "v243"       # out: the claimed counter value (wave 0, lane 0)
+# The unit's output and the next unit's first key tiles, handled after the loop:
+OD = ["v244", "v245", "v246", "v247"]  # output of q-block 0: base lo, base hi; bytes of q-block 0, 1
+OOFF = "v248"        # lane offset of the output rows: (lane % 32) x row stride + 16 (lane / 32)
+S_NK = [("s56", "s57"), ("s58", "s59")]  # next unit's key tiles 0, 1: first byte (lo, hi)
+S_NREC = ["s60", "s61"]  # their bytes (rows x key row stride; 0 reads nothing)
+S_FLAGS = "s62"      # bit 0: prefetch the next unit's key tiles 0 and 1
+S_ODELTA = "s63"     # q-block 1's output base minus q-block 0's, in bytes
 # loop state
 S_J, S_LAST = "s64", "s65"
 S_B = ["s66", "s67", "s68"]        # block ids of tiles j, j+1, j+2 (paged)
@@ -683,6 +695,81 @@ def block_pv_only(em, par):
     em.lds_drain()
 
 
+def block_kprefetch(em, u):
+    """Key tiles 0 and 1 of the next unit into K buffers 0 and 1 (rows
+    16 w .. 16 w + 15 of each, as the loop's fills), when S_FLAGS bit 0 is
+    set.  Every wave has passed the loop's last barrier, after which no wave
+    reads the K buffers."""
+    em(f"s_bitcmp1_b32 {S_FLAGS}, 0")
+    em(f"s_cbranch_scc0 {u}nokpf")
+    for t, rs_w in ((0, S_RK_W), (1, S_RV_W)):
+        lo, hi = S_NK[t]
+        em(f"s_mov_b32 {rs_w[0]}, {lo}")
+        em(f"s_and_b32 {rs_w[1]}, {hi}, 0xffff")
+        em(f"s_mov_b32 {rs_w[2]}, {S_NREC[t]}")
+        em(f"s_mov_b32 {rs_w[3]}, {RSRC_W3}")
+        rsrc = S_RK if t == 0 else S_RV
+        for i in range(4):
+            em(f"s_add_u32 m0, {S_M0W}, {TILE * t + 1024 * i}")
+            em("s_nop 0")
+            em(f"buffer_load_dwordx4 {DMAK[i]}, {rsrc}, 0 offen lds")
+    em(f"{u}nokpf:")
+
+
+def block_output(em):
+    """O^T / l as bf16 rows.  Lane (qc, h) of O[n][qb] register v holds d =
+    32 n + 8 (v / 4) + 4 h + v % 4 of row qc of q-block qb: registers
+    8 half .. 8 half + 7 make two 8-byte pieces, of 16-byte chunks 4 n + 2
+    half (its first 4 values) and 4 n + 2 half + 1, of the lane's row half.
+    v_permlane32_swap_b32 exchanges the second piece of the lanes h = 0 with
+    the first piece of the lanes h = 1, so lane h holds chunk 4 n + 2 half + h
+    whole, stored at row qc, byte 16 (4 n + 2 half + h).  Rows past the
+    q-block's row count (the resource size) are dropped; a row without a
+    visible key (l = 0) is stored as zeros."""
+    em("s_nop 7")  # MFMA results (the last PV) before v_accvgpr_read
+    em("s_nop 7")
+    for qb in range(2):
+        em(f"v_rcp_f32 {AL[qb]}, {LRUN[qb]}")
+    em(f"v_cmp_lt_f32_e64 {S_F0}, 0, {LRUN[0]}")
+    em(f"v_cmp_lt_f32_e64 {S_F1}, 0, {LRUN[1]}")
+    em("s_nop 1")
+    em(f"v_cndmask_b32_e64 {AL[0]}, 0, {AL[0]}, {S_F0}")
+    em(f"v_cndmask_b32_e64 {AL[1]}, 0, {AL[1]}, {S_F1}")
+    # resources of the two q-blocks' rows
+    em(f"v_readfirstlane_b32 {S_RK_W[0]}, {OD[0]}")
+    em(f"v_readfirstlane_b32 {S_RK_W[1]}, {OD[1]}")
+    em(f"v_readfirstlane_b32 {S_RK_W[2]}, {OD[2]}")
+    em(f"v_readfirstlane_b32 {S_RV_W[2]}, {OD[3]}")
+    em("s_nop 4")  # VALU-written SGPRs before SALU and buffer reads
+    em(f"s_add_u32 {S_RV_W[0]}, {S_RK_W[0]}, {S_ODELTA}")
+    em(f"s_addc_u32 {S_RV_W[1]}, {S_RK_W[1]}, 0")
+    em(f"s_and_b32 {S_RK_W[1]}, {S_RK_W[1]}, 0xffff")
+    em(f"s_and_b32 {S_RV_W[1]}, {S_RV_W[1]}, 0xffff")
+    em(f"s_mov_b32 {S_RK_W[3]}, {RSRC_W3}")
+    em(f"s_mov_b32 {S_RV_W[3]}, {RSRC_W3}")
+    t = [f"v{k}" for k in range(8)]
+    groups = [8 + 4 * g for g in range(6)]  # six 4-register pieces, used in turn
+    gi = 0
+    for qb in range(2):
+        rsrc = S_RK if qb == 0 else S_RV
+        for n in range(4):
+            for half in range(2):
+                base = 64 + 16 * (2 * n + qb) + 8 * half
+                for k in range(8):
+                    em(f"v_accvgpr_read_b32 {t[k]}, a{base + k}")
+                for k in range(8):
+                    em(f"v_mul_f32 {t[k]}, {AL[qb]}, {t[k]}")
+                g = groups[gi % len(groups)]
+                gi += 1
+                for e in range(4):
+                    em(f"v_cvt_pk_bf16_f32 v{g + e}, {t[2 * e]}, {t[2 * e + 1]}")
+                em("s_nop 1")
+                em(f"v_permlane32_swap_b32 v{g}, v{g + 2}")
+                em(f"v_permlane32_swap_b32 v{g + 1}, v{g + 3}")
+                em("s_nop 1")
+                em(f"buffer_store_dwordx4 v[{g}:{g + 3}], {OOFF}, {rsrc}, 0 offen offset:{64 * n + 32 * half}")
+
+
 def program(paged):
     em = Emitter()
     u = "L%=_"
@@ -723,8 +810,9 @@ def program(paged):
         block_slow(em, par, f"{u}f{par}")
         block_slow(em, par, f"{u}l{par}")
     em(f"{u}final:")
-    em("s_waitcnt vmcnt(0) lgkmcnt(0)")  # no load may land after the asm
+    em("s_waitcnt vmcnt(0) lgkmcnt(0)")
     em.lds = []
+    block_kprefetch(em, u)
     em(f"s_bitcmp1_b32 {S_LAST}, 0")
     em(f"s_cbranch_scc1 {u}final1")
     block_pv_only(em, 0)
@@ -741,6 +829,7 @@ def program(paged):
     for qb in range(2):
         em(f"v_add_f32 {LRUN[qb]}, {LRUN[qb]}, {ET[qb]}")
     mark(em, 6)
+    block_output(em)
     em("s_nop 7")
     em("s_nop 7")
     em("s_nop 3")
@@ -748,8 +837,8 @@ def program(paged):
 
 
 CLOBBERS = (
-    [f"v{i}" for i in range(0, 192)] + ["v216", "v217"] + [f"v{i}" for i in range(222, 243)]
-    + [f"a{i}" for i in range(192, 256)] + [f"s{i}" for i in range(64, 100)]
+    [f"v{i}" for i in range(0, 192)] + [f"v{i}" for i in range(216, 220)] + [f"v{i}" for i in range(222, 243)]
+    + [f"a{i}" for i in range(64, 256)] + [f"s{i}" for i in range(64, 100)]
     + ["vcc", "scc", "m0", "memory"]
 )
 
