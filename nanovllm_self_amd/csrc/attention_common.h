@@ -103,12 +103,18 @@ struct PlanHeader {
 static_assert(sizeof(PlanHeader) == 256, "plan header is one 256-byte line");
 
 // What a work-group of the MFMA prefill kernel needs to start a list entry,
-// in one 32-byte load: the entry, its sequence's query and key ranges and
-// (paged) the block ids of its first three 64-key tiles (-1: missing).
+// in one 64-byte load: the entry, its sequence's query and key ranges,
+// (paged) the block ids of its first three 64-key tiles (-1: missing), and
+// what the kernel derives from them per entry: the entry's first query
+// position p0, the 64-key tiles its rows see, the key rows its fills may
+// read (local mode: never past the k / v tensors), K - L, the first key row
+// clamped into the local k / v, the sequence and the bytes of its
+// block-table row the kernel may read.
 struct PlanRecord {
   int item, q0, L, k0, K, blk0, blk1, blk2;
+  int p0, ntiles, kf, off, k0c, b, bt_bytes, pad;
 };
-static_assert(sizeof(PlanRecord) == 32, "plan record is 32 bytes");
+static_assert(sizeof(PlanRecord) == 64, "plan record is 64 bytes");
 
 struct Plan {
   PlanHeader* hdr;

@@ -19,6 +19,7 @@ struct PlanArgs {
   int* shadow_base;  // code caches: per-row first tile of the bf16 copy (null: no copy)
   int shadow_cap;
   int shadow_st;     // tiles of a table row: a row's tiles past it are not copied
+  int64_t Tk;        // rows of the local k / v (local mode)
 };
 
 // Tiles of the bf16 copy for a prefill row with kl keys.
@@ -138,9 +139,30 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanArgs a) {
         r.blk1 = a.paged ? tile_block(a, b, kl, 1) : -1;
         r.blk2 = a.paged ? tile_block(a, b, kl, 2) : -1;
       }
+      // What the MFMA kernel derives per entry.  The table it reads is the
+      // copy's (64-key tiles, shadow_st a row) when the copy serves the call.
+      r.off = kl - r.L;
+      r.b = b;
+      if (a.paged) {
+        r.k0c = 0;
+        r.kf = kl;
+        const int tbs = shadow ? kShadowTile : a.bs;
+        const int64_t tst = shadow ? a.shadow_st : a.bt_stride;
+        r.bt_bytes = 4 * (int)min((int64_t)(kl + tbs - 1) / tbs, tst);
+      } else {
+        const int64_t k0c = min(max((int64_t)k0, (int64_t)0), a.Tk);
+        r.k0c = (int)k0c;
+        r.kf = (int)max((int64_t)0, min((int64_t)kl, a.Tk - k0c));
+        r.bt_bytes = 0;
+      }
+      r.pad = 0;
       for (int i = 0; i < np; ++i) {
         const int e = base + incl - np + i;
         r.item = b * pl.ntq + (np - 1 - i);
+        r.p0 = (np - 1 - i) * pl.pbm;
+        const int p_last = min(r.L, r.p0 + pl.pbm) - 1;
+        const int kv_end = min(kl, p_last + r.off + 1);
+        r.ntiles = (r.p0 < r.L && kv_end > 0) ? (kv_end + 63) / 64 : 0;
         pl.plist[e] = r.item;
         pl.rec[e] = r;
       }
@@ -179,6 +201,7 @@ int launch_plan(const AttnParams& P, const Plan& plan, bool paged, hipStream_t s
   a.shadow_base = shadow ? shadow->base : nullptr;
   a.shadow_cap = shadow ? shadow->cap : 0;
   a.shadow_st = shadow ? shadow->ST : 0;
+  a.Tk = P.Tk;
   hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(1024), 0, stream, a);
   return check_launch("plan");
 }

@@ -242,7 +242,7 @@ def test_c_abi_validates_before_launch():
 
 
 def test_workspace_bytes():
-    """The prefill plan (256-byte header + prefill list + a 32-byte record
+    """The prefill plan (256-byte header + prefill list + a 64-byte record
     per list entry, each 256-aligned) followed by the decode partials: two slots of g x (128 + 2) floats per decode
     wave, then a 4-int header and a 4-int merge record per decode wave
     (for the 2048-wave cap).  Decode waves come in groups of Hkv: at most 2048 waves, and at
@@ -261,19 +261,19 @@ def test_workspace_bytes():
         gg = Hq // Hkv if Hkv > 0 and Hq % Hkv == 0 else 0
         pbm = 32 * (8 // min(gg, 8)) if gg > 0 else 32
         ntq = max(1, (max_q + pbm - 1) // pbm)
-        return a256(256 + a256(B * ntq * 4) + a256(B * ntq * 32)) + waves * 2 * g * 130 * 4 + 2049 * 16
+        return a256(256 + a256(B * ntq * 4) + a256(B * ntq * 64)) + waves * 2 * g * 130 * 4 + 2049 * 16
 
     # 64 decode rows, max_k 256: 512 tiles -> 128 groups of 8 waves
     assert lib.nvs_attention_workspace_bytes(64, 1, 256, 32, 8, 128, 256) == expect(64, 1, 256, 32, 8)
-    assert expect(64, 1, 256, 32, 8) == a256(256 + a256(64 * 4) + a256(64 * 32)) + 1024 * 2 * 4 * 130 * 4 + 2049 * 16
+    assert expect(64, 1, 256, 32, 8) == a256(256 + a256(64 * 4) + a256(64 * 64)) + 1024 * 2 * 4 * 130 * 4 + 2049 * 16
     # max_k 8192: the 2048-wave cap
     assert lib.nvs_attention_workspace_bytes(64, 1, 8192, 32, 8, 128, 256) == expect(64, 1, 8192, 32, 8)
-    assert expect(64, 1, 8192, 32, 8) == a256(256 + a256(64 * 4) + a256(64 * 32)) + 2048 * 2 * 4 * 130 * 4 + 2049 * 16
+    assert expect(64, 1, 8192, 32, 8) == a256(256 + a256(64 * 4) + a256(64 * 64)) + 2048 * 2 * 4 * 130 * 4 + 2049 * 16
     # prefill tiles: 32 positions per wave, 8 waves shared by the g query heads
     # of a kv head -> 64 positions at g = 4, 32 at g >= 8, 256 at g = 1
     for Hq, Hkv in ((32, 8), (64, 4), (8, 8), (32, 0)):
         assert lib.nvs_attention_workspace_bytes(16, 4096, 256, Hq, Hkv, 128, 256) == expect(16, 4096, 256, Hq, Hkv)
-    assert expect(16, 4096, 256, 32, 8) == a256(256 + a256(16 * 64 * 4) + a256(16 * 64 * 32)) + 256 * 2 * 4 * 520 + 2049 * 16
+    assert expect(16, 4096, 256, 32, 8) == a256(256 + a256(16 * 64 * 4) + a256(16 * 64 * 64)) + 256 * 2 * 4 * 520 + 2049 * 16
 
 
 def test_workspace_unknown_kv_heads_is_upper_bound():
