@@ -4,6 +4,7 @@
 
 #include "nvs_common.h"
 #include "attention_common.h"
+#include "decode_merge.h"
 
 using namespace nvs;
 
@@ -184,10 +185,13 @@ static int paged_attention_impl(AttnParams& P, const void* q, int64_t q_tok_stri
                            : make_plan(workspace, P);
   char* partials = (char*)workspace + align256(plan_bytes(num_seqs, plan.ntq));
   const int max_waves = decode_wave_cap(num_seqs, max_seqlen_k, num_kv_heads);
-  rc = launch_decode(P, max_waves, decode_launch_waves(max_waves, num_kv_heads), partials, s);
+  // With prefill rows the plan launch also merges the split decode rows.
+  MergeJob merge;
+  rc = launch_decode(P, max_waves, decode_launch_waves(max_waves, num_kv_heads), partials, s,
+                     max_seqlen_q > 1 ? &merge : nullptr);
   if (rc != NVS_OK || max_seqlen_q == 1) return rc;  // no prefill rows: no plan
   if (!shadow) {
-    rc = launch_plan(P, plan, /*paged=*/true, s);
+    rc = launch_plan(P, plan, /*paged=*/true, s, nullptr, &merge);
     if (rc != NVS_OK) return rc;
     return launch_prefill_any(P, plan, s);
   }
@@ -197,7 +201,7 @@ static int paged_attention_impl(AttnParams& P, const void* q, int64_t q_tok_stri
   const ShadowLayout sh = shadow_at((char*)workspace + align256(attention_workspace_bytes(
                                         P.B, P.max_seqlen_q, P.max_seqlen_k, P.Hq, P.Hkv)),
                                     P.B, P.max_seqlen_k, P.Hkv);
-  rc = launch_plan(P, plan, /*paged=*/true, s, &sh);
+  rc = launch_plan(P, plan, /*paged=*/true, s, &sh, &merge);
   if (rc != NVS_OK) return rc;
   rc = launch_shadow_fill(P, plan, sh, s);
   if (rc != NVS_OK) return rc;

@@ -256,12 +256,18 @@ int64_t attention_workspace_bytes(int num_seqs, int max_seqlen_q, int max_seqlen
 // bound (max_waves) and the device's resident wave slots, whichever is
 // smaller.
 int decode_launch_waves(int max_waves, int Hkv);
+struct MergeJob;
+// The plan kernel; with `merge` it also runs the decode launch's merge of
+// split rows (extra work-groups beside the plan's).
 int launch_plan(const AttnParams& P, const Plan& plan, bool paged, hipStream_t stream,
-                const ShadowLayout* shadow = nullptr);
+                const ShadowLayout* shadow = nullptr, const MergeJob* merge = nullptr);
 // Dequantises the prefill rows' tiles into the copy (runs only where the
 // plan set shadow_on).
 int launch_shadow_fill(const AttnParams& P, const Plan& plan, const ShadowLayout& sh, hipStream_t stream);
-int launch_decode(const AttnParams& P, int max_waves, int waves, void* partials, hipStream_t stream);
+// The decode kernel, then the merge of split rows: its own launch, or, with
+// `defer`, left to the plan launch (defer receives what it needs).
+int launch_decode(const AttnParams& P, int max_waves, int waves, void* partials, hipStream_t stream,
+                  MergeJob* defer = nullptr);
 int launch_prefill(const AttnParams& P, const Plan& plan, hipStream_t stream);
 // The MFMA tile-loop prefill kernel (paged_prefill_mx.hip): whether it serves
 // a call, its query positions per work item for a group of g query heads,

@@ -41,38 +41,10 @@
 #include "nvs_common.h"
 #include "attention_common.h"
 #include "store_common.h"
+#include "decode_merge.h"
 
 namespace nvs {
 
-struct DecodeArgs {
-  const uint16_t* q;
-  int64_t q_ts, q_hs;
-  const void* kc;
-  const void* vc;
-  const float* ks;
-  const float* vs;
-  int bt_stride;  // row stride == number of columns
-  int NB;
-  int Hq, Hkv, g, bs;
-  float scale_log2;
-  float* ws_o;   // [max_waves, 2 slots, g, 128]
-  float* ws_ml;  // [max_waves, 2 slots, g, 2]
-  int32_t* ws_rec;  // [4 + 4 waves]: (T, Kw), then per wave the split row it merges
-  // New tokens (bf16) stored by the decode waves themselves: copied into a
-  // bf16 cache, quantised per token and kv head into an fp8 / int8 one with
-  // their scales into ks / vs (kn null: none).
-  const uint16_t* kn;
-  const uint16_t* vn;
-  int64_t kn_ts, kn_hs, vn_ts, vn_hs;
-  const int32_t* slots;
-  int64_t total_slots;
-  const int32_t* cu_q;
-  const int32_t* cu_k;
-  int B;
-  int64_t T;  // query / output rows
-  uint16_t* out;
-  int64_t out_ts, out_hs;
-};
 
 // Registers of one 32-key tile as loaded from HBM.  `has` is false when the
 // tile's block-table entry is missing (< 0 or outside the pool); the loads
@@ -780,7 +752,6 @@ __device__ __forceinline__ int decode_groups(int T, int G) {
   return T > 0 ? min(G, max(1, T / kDecodeMinUnits)) : 0;
 }
 
-__device__ __forceinline__ int group_start(int T, int Kw, int k) { return (int)((int64_t)k * T / Kw); }
 
 // One decode wave (kv head h of group k): tiles [s0, s0 + left) of the
 // stream, streamed one by one, partials at index w.  Cursor n[0] is
@@ -950,66 +921,10 @@ void paged_decode_kernel(DecodeArgs a, const int32_t* __restrict__ bt, const int
   }
 }
 
-// Log-sum-exp merge of the rows split across groups.  Wave k Hkv + h owns kv
-// head h of the row recorded by decode wave k Hkv + h (the row that crosses
-// the boundary after group k and starts inside group k's range); its
-// partials sit in wave
-// k Hkv + h (the recorded slot) and in waves x Hkv + h for groups x = k + 1
-// .. k_last (slot 0).  Lane l serves head 4 p + l / 16 of the group (pass p)
-// and head_dim elements 8 (l % 16) .. + 7; one pass over the partials keeps
-// a running max, sum and output, with the loads of four partials in flight
-// at a time.
+// The merge of split rows as a launch of its own (decode-only calls); calls
+// with prefill rows run it in the plan launch (merge_split_row).
 __global__ __launch_bounds__(64) void decode_merge_kernel(DecodeArgs a) {
-  const int k = blockIdx.x / a.Hkv, h = blockIdx.x - k * a.Hkv;
-  const int lane = threadIdx.x;
-  const int32_t* rec = a.ws_rec + 4 + 4 * blockIdx.x;
-  if (__builtin_amdgcn_readfirstlane(rec[3]) == 0) return;
-  const int T = __builtin_amdgcn_readfirstlane(a.ws_rec[0]);
-  const int Kw = __builtin_amdgcn_readfirstlane(a.ws_rec[1]);
-  const int q_row = __builtin_amdgcn_readfirstlane(rec[0]);
-  const int last = group_start(T, Kw, k + 1) - 1 + __builtin_amdgcn_readfirstlane(rec[1]);  // the row's last tile
-  const int k_last = (int)(((int64_t)(last + 1) * Kw - 1) / T);
-  const int slot_k = __builtin_amdgcn_readfirstlane(rec[2]);
-  const int j = lane & 15;
-  for (int c0 = 0; c0 < a.g; c0 += 4) {
-    const int c = c0 + (lane >> 4);
-    const bool use = c < a.g;
-    const int cc = use ? c : 0;
-    float M = -INFINITY, L = 0.0f;
-    f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-    for (int x0 = k; x0 <= k_last; x0 += 4) {
-      f32x2 ml[4];
-      f32x4 o0[4], o1[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int x = min(x0 + u, k_last);
-        const int64_t base = (((int64_t)x * a.Hkv + h) * 2 + (x == k ? slot_k : 0)) * a.g + cc;
-        ml[u] = *reinterpret_cast<const f32x2*>(a.ws_ml + base * 2);
-        o0[u] = *reinterpret_cast<const f32x4*>(a.ws_o + base * kHeadDim + 8 * j);
-        o1[u] = *reinterpret_cast<const f32x4*>(a.ws_o + base * kHeadDim + 8 * j + 4);
-      }
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        if (x0 + u > k_last) break;
-        const float m_new = fmaxf(M, ml[u][0]);
-        const float al = M == -INFINITY ? 0.0f : fast_exp2(M - m_new);
-        const float be = ml[u][0] == -INFINITY ? 0.0f : fast_exp2(ml[u][0] - m_new);
-        M = m_new;
-        L = L * al + ml[u][1] * be;
-        acc0 = acc0 * al + o0[u] * be;
-        acc1 = acc1 * al + o1[u] * be;
-      }
-    }
-    if (use) {
-      const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-      u32x4 v;
-      v[0] = pack_bf16x2(acc0[0] * inv, acc0[1] * inv);
-      v[1] = pack_bf16x2(acc0[2] * inv, acc0[3] * inv);
-      v[2] = pack_bf16x2(acc1[0] * inv, acc1[1] * inv);
-      v[3] = pack_bf16x2(acc1[2] * inv, acc1[3] * inv);
-      *reinterpret_cast<u32x4*>(a.out + (int64_t)q_row * a.out_ts + (int64_t)(h * a.g + c) * a.out_hs + 8 * j) = v;
-    }
-  }
+  merge_split_row(a, blockIdx.x, threadIdx.x);
 }
 
 int64_t decode_workspace_bytes(int max_waves, int group) {
@@ -1019,7 +934,9 @@ int64_t decode_workspace_bytes(int max_waves, int group) {
          ((int64_t)kDecodeMaxWaves + 1) * 4 * (int64_t)sizeof(int32_t);
 }
 
-int launch_decode(const AttnParams& P, int max_waves, int waves, void* partials, hipStream_t stream) {
+int launch_decode(const AttnParams& P, int max_waves, int waves, void* partials, hipStream_t stream,
+                  MergeJob* defer) {
+  if (defer) defer->units = 0;
   DecodeArgs a;
   a.q = (const uint16_t*)P.q; a.q_ts = P.q_ts; a.q_hs = P.q_hs;
   a.kc = P.kc; a.vc = P.vc; a.ks = P.ks; a.vs = P.vs;
@@ -1056,6 +973,11 @@ int launch_decode(const AttnParams& P, int max_waves, int waves, void* partials,
   // With one group no row is split (keyless rows were zeroed by the decode
   // kernel's scan).
   const int groups = waves / P.Hkv;
+  if (defer) {  // the plan launch runs the merge
+    defer->a = a;
+    defer->units = groups > 1 ? (groups - 1) * P.Hkv : 0;
+    return NVS_OK;
+  }
   if (groups <= 1) return NVS_OK;
   hipLaunchKernelGGL(decode_merge_kernel, dim3((groups - 1) * P.Hkv), dim3(64), 0, stream, a);
   return check_launch("decode_merge");

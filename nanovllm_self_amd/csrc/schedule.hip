@@ -2,6 +2,7 @@
 // without a host round trip.
 #include "nvs_common.h"
 #include "attention_common.h"
+#include "decode_merge.h"
 
 namespace nvs {
 
@@ -81,16 +82,28 @@ __device__ __forceinline__ void row_work(const PlanArgs& a, int b, bool& dec, in
 constexpr int kPlanThreads = 1024;
 constexpr int kPlanWaves = kPlanThreads / 64;
 
-__global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanArgs a) {
+// What the plan keeps of each row of a 1024-row step in LDS while the
+// step's list entries are written, one entry per thread.
+struct PlanRows {
+  int end[kPlanThreads];  // inclusive prefix of the rows' entry counts
+  int q0[kPlanThreads], L[kPlanThreads], k0[kPlanThreads], K[kPlanThreads];
+  int blk[3][kPlanThreads];
+};
+
+// Work-group 0 writes the plan; the others (a paged call whose decode
+// launch left its merge to this one) merge the decode rows split across
+// groups, one merge wave per wave.
+__global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanArgs a, DecodeArgs m, int merge_units) {
+  if (blockIdx.x > 0) {
+    const int unit = (blockIdx.x - 1) * kPlanWaves + (threadIdx.x >> 6);
+    if (unit < merge_units) merge_split_row(m, __builtin_amdgcn_readfirstlane(unit), threadIdx.x & 63);
+    return;
+  }
   __shared__ int scan_lds[kPlanWaves];
+  __shared__ PlanRows rows;
   const int tid = threadIdx.x;
   const Plan& pl = a.plan;
   if (tid < 8) pl.hdr->prefill_next[tid] = 0;
-  // ---- prefill tiles row by row (1024 rows per step: an exclusive scan of
-  // the rows' tile counts), each row's tiles deepest first (most keys under
-  // the causal mask).  Row-major order keeps the work-groups of an XCD on the
-  // same sequence at the same time, so the K/V tiles they all read come
-  // from HBM once and from L2 after that.
   // ---- code caches: the prefill rows' 64-key tiles of the bf16 copy, row
   // by row (an exclusive scan of ceil(k_len / 64)); the copy serves the call
   // if they fit.
@@ -116,57 +129,75 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanArgs a) {
     pl.hdr->shadow_tiles = 0;
     pl.hdr->shadow_on = 0;
   }
+  // ---- prefill tiles row by row (1024 rows per step: a scan of the rows'
+  // tile counts), each row's tiles deepest first (most keys under the causal
+  // mask).  Row-major order keeps the work-groups of an XCD on the same
+  // sequence at the same time, so the K/V tiles they all read come from HBM
+  // once and from L2 after that.  Each thread then writes entries e, e +
+  // 1024, ... of the step, finding its row by a binary search of the prefix.
   int base = 0;
   for (int b0 = 0; b0 < a.B; b0 += kPlanThreads) {
     bool dec;
     int np, q0, kl, tot;
-    row_work(a, b0 + tid, dec, np, q0, kl);
+    const int b = b0 + tid;
+    row_work(a, b, dec, np, q0, kl);
     const int incl = block_scan_1024(np, scan_lds, tot);
+    rows.end[tid] = incl;
     if (np > 0) {
-      const int b = b0 + tid, k0 = a.cu_k[b];
-      PlanRecord r;
-      r.q0 = q0;
-      r.L = a.cu_q[b + 1] - q0;
-      r.k0 = k0;
-      r.K = kl;
+      rows.q0[tid] = q0;
+      rows.L[tid] = a.cu_q[b + 1] - q0;
+      rows.k0[tid] = a.cu_k[b];
+      rows.K[tid] = kl;
       if (shadow) {  // tiles of the copy (the thread wrote shadow_base[b] itself)
         const int sb = a.shadow_base[b], nt = shadow_row_tiles(a, np, kl);
-        r.blk0 = 0 < nt ? sb : -1;
-        r.blk1 = 1 < nt ? sb + 1 : -1;
-        r.blk2 = 2 < nt ? sb + 2 : -1;
+        for (int t = 0; t < 3; ++t) rows.blk[t][tid] = t < nt ? sb + t : -1;
       } else {
-        r.blk0 = a.paged ? tile_block(a, b, kl, 0) : -1;
-        r.blk1 = a.paged ? tile_block(a, b, kl, 1) : -1;
-        r.blk2 = a.paged ? tile_block(a, b, kl, 2) : -1;
-      }
-      // What the MFMA kernel derives per entry.  The table it reads is the
-      // copy's (64-key tiles, shadow_st a row) when the copy serves the call.
-      r.off = kl - r.L;
-      r.b = b;
-      if (a.paged) {
-        r.k0c = 0;
-        r.kf = kl;
-        const int tbs = shadow ? kShadowTile : a.bs;
-        const int64_t tst = shadow ? a.shadow_st : a.bt_stride;
-        r.bt_bytes = 4 * (int)min((int64_t)(kl + tbs - 1) / tbs, tst);
-      } else {
-        const int64_t k0c = min(max((int64_t)k0, (int64_t)0), a.Tk);
-        r.k0c = (int)k0c;
-        r.kf = (int)max((int64_t)0, min((int64_t)kl, a.Tk - k0c));
-        r.bt_bytes = 0;
-      }
-      r.pad = 0;
-      for (int i = 0; i < np; ++i) {
-        const int e = base + incl - np + i;
-        r.item = b * pl.ntq + (np - 1 - i);
-        r.p0 = (np - 1 - i) * pl.pbm;
-        const int p_last = min(r.L, r.p0 + pl.pbm) - 1;
-        const int kv_end = min(kl, p_last + r.off + 1);
-        r.ntiles = (r.p0 < r.L && kv_end > 0) ? (kv_end + 63) / 64 : 0;
-        pl.plist[e] = r.item;
-        pl.rec[e] = r;
+        for (int t = 0; t < 3; ++t) rows.blk[t][tid] = a.paged ? tile_block(a, b, kl, t) : -1;
       }
     }
+    __syncthreads();
+    for (int e = tid; e < tot; e += kPlanThreads) {
+      int lo = 0, hi = kPlanThreads - 1;  // the first row whose prefix passes e
+      while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (rows.end[mid] > e) hi = mid; else lo = mid + 1;
+      }
+      const int r = lo, rb = b0 + r;
+      const int qt = rows.end[r] - 1 - e;  // the row's first entry is its deepest tile
+      PlanRecord rec;
+      rec.q0 = rows.q0[r];
+      rec.L = rows.L[r];
+      rec.k0 = rows.k0[r];
+      rec.K = rows.K[r];
+      rec.blk0 = rows.blk[0][r];
+      rec.blk1 = rows.blk[1][r];
+      rec.blk2 = rows.blk[2][r];
+      // What the MFMA kernel derives per entry.  The table it reads is the
+      // copy's (64-key tiles, shadow_st a row) when the copy serves the call.
+      rec.off = rec.K - rec.L;
+      rec.b = rb;
+      if (a.paged) {
+        rec.k0c = 0;
+        rec.kf = rec.K;
+        const int tbs = shadow ? kShadowTile : a.bs;
+        const int64_t tst = shadow ? a.shadow_st : a.bt_stride;
+        rec.bt_bytes = 4 * (int)min((int64_t)(rec.K + tbs - 1) / tbs, tst);
+      } else {
+        const int64_t k0c = min(max((int64_t)rec.k0, (int64_t)0), a.Tk);
+        rec.k0c = (int)k0c;
+        rec.kf = (int)max((int64_t)0, min((int64_t)rec.K, a.Tk - k0c));
+        rec.bt_bytes = 0;
+      }
+      rec.pad = 0;
+      rec.item = rb * pl.ntq + qt;
+      rec.p0 = qt * pl.pbm;
+      const int p_last = min(rec.L, rec.p0 + pl.pbm) - 1;
+      const int kv_end = min(rec.K, p_last + rec.off + 1);
+      rec.ntiles = (rec.p0 < rec.L && kv_end > 0) ? (kv_end + 63) / 64 : 0;
+      pl.plist[base + e] = rec.item;
+      pl.rec[base + e] = rec;
+    }
+    __syncthreads();  // the next step's rows overwrite the LDS
     base += tot;
   }
   if (tid == 0) pl.hdr->n_prefill = base;
@@ -186,7 +217,8 @@ int device_slots(int per_cu) {
   return g_cus[dev] * per_cu;
 }
 
-int launch_plan(const AttnParams& P, const Plan& plan, bool paged, hipStream_t stream, const ShadowLayout* shadow) {
+int launch_plan(const AttnParams& P, const Plan& plan, bool paged, hipStream_t stream, const ShadowLayout* shadow,
+                const MergeJob* merge) {
   PlanArgs a;
   a.cu_q = P.cu_q;
   a.cu_k = P.cu_k;
@@ -202,7 +234,14 @@ int launch_plan(const AttnParams& P, const Plan& plan, bool paged, hipStream_t s
   a.shadow_cap = shadow ? shadow->cap : 0;
   a.shadow_st = shadow ? shadow->ST : 0;
   a.Tk = P.Tk;
-  hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(1024), 0, stream, a);
+  DecodeArgs m = {};
+  int units = 0;
+  if (merge && merge->units > 0) {
+    m = merge->a;
+    units = merge->units;
+  }
+  const int grid = 1 + (units + kPlanWaves - 1) / kPlanWaves;
+  hipLaunchKernelGGL(plan_kernel, dim3(grid), dim3(kPlanThreads), 0, stream, a, m, units);
   return check_launch("plan");
 }
 
