@@ -27,6 +27,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import statistics
 import sys
 import time
 
@@ -60,6 +61,24 @@ def timed_steps(fn, steps: int, warmup: int):
     return wall, e0.elapsed_time(e1) / steps
 
 
+def paired_steps(step_fn, attn_fn, steps: int, warmup: int, reps: int = 3):
+    """A batch's attention-only call and its whole step (store + attention),
+    timed in alternating blocks (attention, step, attention, ...), each block
+    W untimed calls then K timed ones, `reps` blocks of each.  Returns the
+    medians of (step wall ms, step event ms, attention event ms).  The first
+    block after a workload is built runs several percent slower than later
+    ones while the clock settles; alternating keeps that out of the
+    difference between the two."""
+    sw, se, ae = [], [], []
+    for _ in range(reps):
+        ae.append(timed_steps(attn_fn, steps, warmup)[1])
+        w, e = timed_steps(step_fn, steps, warmup)
+        sw.append(w)
+        se.append(e)
+    med = statistics.median
+    return med(sw), med(se), med(ae)
+
+
 def attention_only(wl):
     a = wl.attn
     fn = a.prefill_flashattn if a.forward_backend in ("flashattn", "hip") else a.prefill_torch
@@ -76,8 +95,8 @@ def bench_decode(steps, warmup, cpu=False):
     log("building decode_8b (bf16)")
     wl = W.decode_8b("cuda")
     nbytes = wl.decode_bytes()
-    ms_step, _ = timed_steps(step(wl), steps, warmup)
     _, ms_attn = timed_steps(attention_only(wl), steps, warmup)
+    ms_step, _ = timed_steps(step(wl), steps, warmup)
     res = {
         "bytes": nbytes,
         "ms_per_step": ms_step,
@@ -209,13 +228,13 @@ def bench_prefill(steps, warmup, cpu=False):
     log("building prefill_8b")
     wl = W.prefill_8b("cuda")
     flops = wl.prefill_flops()
-    ms_step, _ = timed_steps(step(wl), steps, warmup)
-    _, ms_attn = timed_steps(attention_only(wl), steps, warmup)
+    ms_step, ms_step_ev, ms_attn = paired_steps(step(wl), attention_only(wl), steps, warmup)
     res = {
         "workload": "prefill_8b: 32q/8kv heads, D128, bs256, 16 seqs, new U[512,4096] over 0-8 cached blocks, seed 2",
         "flops": flops,
         "ms_per_step": ms_step,
         "ms_attention": ms_attn,
+        "step_minus_attention_us": (ms_step_ev - ms_attn) * 1e3,  # both by HIP events
         "tflops": flops / ms_attn / 1e9,
         "frac_bf16_peak": flops / ms_attn / 1e9 / BF16_PEAK_TFLOPS,
         "tokens_per_s": sum(s.num_new_tokens for s in wl.seqs) / (ms_step / 1e3),
@@ -230,8 +249,7 @@ def bench_prefill(steps, warmup, cpu=False):
     # dequantised into a bf16 copy and the tile-loop kernel runs on it.
     log("building prefill_8b (fp8 cache)")
     wl = W.prefill_8b("cuda", kv="fp8")
-    ms_step8, _ = timed_steps(step(wl), steps, warmup)
-    _, ms_attn8 = timed_steps(attention_only(wl), steps, warmup)
+    ms_step8, _, ms_attn8 = paired_steps(step(wl), attention_only(wl), steps, warmup)
     res["fp8_cache"] = {
         "ms_per_step": ms_step8,
         "ms_attention": ms_attn8,
@@ -252,8 +270,7 @@ def bench_quant(steps, warmup, cpu=False):
         log(f"building decode_quant ({kv})")
         wl = W.decode_quant("cuda", kv=kv)
         nbytes = wl.decode_bytes()
-        ms_step, _ = timed_steps(step(wl), steps, warmup)
-        _, ms_attn = timed_steps(attention_only(wl), steps, warmup)
+        ms_step, _, ms_attn = paired_steps(step(wl), attention_only(wl), steps, warmup)
         out[kv] = {
             "bytes": nbytes,
             "ms_per_step": ms_step,
@@ -473,11 +490,12 @@ def bench_mixed(steps, warmup, cpu=False):
     for kv in ("bf16", "fp8"):
         log(f"building mixed_32b ({kv})")
         wl = W.mixed_32b("cuda", kv=kv)
-        ms_step, _ = timed_steps(step(wl), steps, warmup)
+        ms_step, _, ms_attn = paired_steps(step(wl), attention_only(wl), steps, warmup)
         dec_b, pf = wl.decode_bytes(), wl.prefill_flops()
         t_roof = dec_b / (HBM_PEAK_GBS * 1e9) + pf / (BF16_PEAK_TFLOPS * 1e12)
         out[kv] = {
             "ms_per_step": ms_step,
+            "ms_attention": ms_attn,
             "decode_bytes": dec_b,
             "prefill_flops": pf,
             "roofline_ms": t_roof * 1e3,

@@ -216,7 +216,8 @@ int64_t nvs_attention_workspace_bytes_cache(int num_seqs, int max_seqlen_q,
  * flash_attn_varlen_func(..., block_table=...)) and equally the
  * prefix branch of prefill_torch (attention.py:441-498).  Serves prefix-hit
  * prefill, chunked prefill, decode (q_len == 1) and mixed batches in one call.
- *   q             [num_tokens, num_heads, head_dim] BF16, strides in elements.
+ *   q             [num_tokens, num_heads, head_dim] BF16 (FP16 with an FP16
+ *                 cache), strides in elements.
  *   cu_seqlens_q  [num_seqs + 1] int32 prefix sums of the new-token counts.
  *   cu_seqlens_k  [num_seqs + 1] int32 prefix sums of the visible KV lengths
  *                 (cached prefix + new tokens, already written to the cache).
@@ -232,8 +233,12 @@ int64_t nvs_attention_workspace_bytes_cache(int num_seqs, int max_seqlen_q,
  *   attends keys j <= r + (k_len - q_len) (bottom-right causal); rows with no
  *   visible key produce 0.  GQA: query head hq reads kv head
  *   hq / (num_heads / num_kv_heads).
- *   cache_dtype   BF16, INT8 or FP8_E4M3 (scales required for the last two).
- *   out           [num_tokens, num_heads, head_dim] BF16.
+ *   cache_dtype   BF16, FP16, INT8 or FP8_E4M3 (scales required for the last
+ *                 two).  An FP16 cache computes in fp16 (q, P and out fp16,
+ *                 fp16 MFMA), as the reference's flash path computes in the
+ *                 cache's dtype (attention.py:326-336); the others in bf16.
+ *   out           [num_tokens, num_heads, head_dim] BF16 (FP16 with an FP16
+ *                 cache).
  *   Rows with q_len == 1 run the split-K decode kernels, the others the MFMA
  *   prefill kernel; `workspace` holds at least
  *   nvs_attention_workspace_bytes(...) bytes.
@@ -346,6 +351,25 @@ int nvs_varlen_attention(const void* q, int64_t q_tok_stride,
                          void* out, int64_t out_tok_stride,
                          int64_t out_head_stride, void* workspace,
                          int64_t workspace_bytes, void* stream);
+
+/*
+ * nvs_varlen_attention with the element type of q, k, v and out given:
+ * dtype BF16 or FP16 (fp16 compute, the reference's flash_attn_varlen_func
+ * on fp16 tensors, attention.py:338-354 with attention_compute_dtype
+ * float16).  nvs_varlen_attention is this call with dtype BF16.
+ */
+int nvs_varlen_attention_dtype(const void* q, int64_t q_tok_stride,
+                               int64_t q_head_stride, const void* k, const void* v,
+                               int64_t k_tok_stride, int64_t k_head_stride,
+                               int64_t v_tok_stride, int64_t v_head_stride,
+                               const int32_t* cu_seqlens_q,
+                               const int32_t* cu_seqlens_k, int num_seqs,
+                               int64_t num_tokens, int64_t num_kv_tokens,
+                               int max_seqlen_q, int max_seqlen_k, int num_heads,
+                               int num_kv_heads, int head_dim, float softmax_scale,
+                               void* out, int64_t out_tok_stride,
+                               int64_t out_head_stride, void* workspace,
+                               int64_t workspace_bytes, void* stream, int dtype);
 
 /*
  * Step metadata built on the device.  Replaces the per-token loops of

@@ -111,6 +111,18 @@ SIGNATURES = {
             _P, _L, _P,  # workspace, bytes, stream
         ],
     ),
+    "nvs_varlen_attention_dtype": (
+        _I,
+        [
+            _P, _L, _L,  # q
+            _P, _P, _L, _L, _L, _L,  # k, v
+            _P, _P, _I, _L, _L, _I, _I,  # cu_q, cu_k, num_seqs, num_tokens, num_kv_tokens, max_q, max_k
+            _I, _I, _I, _F,  # heads, kv heads, head_dim, scale
+            _P, _L, _L,  # out
+            _P, _L, _P,  # workspace, bytes, stream
+            _I,  # dtype of q, k, v, out
+        ],
+    ),
     "nvs_build_context": (
         _I,
         [

@@ -71,6 +71,17 @@ static Plan make_plan(void* ws, const AttnParams& P) {
   return plan_at(ws, P.B, prefill_tiles(P.max_seqlen_q, pbm), pbm);
 }
 
+// fp16 elements run only on the tile-loop kernel (the classic kernel is
+// bf16 and code caches); a call it does not serve is refused before any
+// launch.
+static int check_f16_served(const AttnParams& P, const char* who) {
+  NVS_REQUIRE(P.cache_dtype != NVS_DTYPE_FP16 || P.max_seqlen_q <= 1 || prefill_mx_serves(P),
+              NVS_ERR_UNSUPPORTED,
+              "%s: fp16 prefill runs on the tile-loop kernel only, which does not serve this call "
+              "(NVS_PREFILL_KERNEL=classic, or strides past its 32-bit lane offsets)", who);
+  return NVS_OK;
+}
+
 static int launch_prefill_any(const AttnParams& P, const Plan& plan, hipStream_t s) {
   return prefill_mx_serves(P) ? launch_prefill_mx(P, plan, s) : launch_prefill(P, plan, s);
 }
@@ -157,9 +168,9 @@ static int paged_attention_impl(AttnParams& P, const void* q, int64_t q_tok_stri
               "paged_attention: head_dim must be %d, got %d", kHeadDim, head_dim);
   NVS_REQUIRE(k_cache && v_cache && block_tables, NVS_ERR_INVALID,
               "paged_attention: null cache / block_tables pointer");
-  NVS_REQUIRE(cache_dtype == NVS_DTYPE_BF16 || cache_dtype == NVS_DTYPE_INT8 ||
+  NVS_REQUIRE(cache_dtype == NVS_DTYPE_BF16 || cache_dtype == NVS_DTYPE_FP16 || cache_dtype == NVS_DTYPE_INT8 ||
                   cache_dtype == NVS_DTYPE_FP8_E4M3,
-              NVS_ERR_UNSUPPORTED, "paged_attention: cache dtype %d not served (bf16/int8/fp8)",
+              NVS_ERR_UNSUPPORTED, "paged_attention: cache dtype %d not served (bf16/fp16/int8/fp8)",
               cache_dtype);
   NVS_REQUIRE(!is_quant(cache_dtype) || (k_scale && v_scale), NVS_ERR_INVALID,
               "paged_attention: quantised cache needs k_scale and v_scale");
@@ -177,6 +188,8 @@ static int paged_attention_impl(AttnParams& P, const void* q, int64_t q_tok_stri
               NVS_ERR_UNSUPPORTED, "paged_attention: batch too large for one call (decode tiles exceed 2^31)");
   if (max_seqlen_q <= 0) return NVS_OK;
   rc = check_workspace(P, "paged_attention");
+  if (rc != NVS_OK) return rc;
+  rc = check_f16_served(P, "paged_attention");
   if (rc != NVS_OK) return rc;
   hipStream_t s = (hipStream_t)stream;
   const bool shadow = shadow_serves(P);
@@ -278,17 +291,17 @@ extern "C" int nvs_paged_attention_store(const void* q, int64_t q_tok_stride, in
                               workspace_bytes, stream);
 }
 
-extern "C" int nvs_varlen_attention(const void* q, int64_t q_tok_stride, int64_t q_head_stride,
-                                    const void* k, const void* v, int64_t k_tok_stride,
-                                    int64_t k_head_stride, int64_t v_tok_stride,
-                                    int64_t v_head_stride, const int32_t* cu_seqlens_q,
-                                    const int32_t* cu_seqlens_k, int num_seqs, int64_t num_tokens,
-                                    int64_t num_kv_tokens, int max_seqlen_q, int max_seqlen_k, int num_heads,
-                                    int num_kv_heads, int head_dim, float softmax_scale, void* out,
-                                    int64_t out_tok_stride, int64_t out_head_stride,
-                                    void* workspace, int64_t workspace_bytes, void* stream) {
-  clear_error();
+static int varlen_attention_impl(const void* q, int64_t q_tok_stride, int64_t q_head_stride,
+                                 const void* k, const void* v, int64_t k_tok_stride,
+                                 int64_t k_head_stride, int64_t v_tok_stride,
+                                 int64_t v_head_stride, const int32_t* cu_seqlens_q,
+                                 const int32_t* cu_seqlens_k, int num_seqs, int64_t num_tokens,
+                                 int64_t num_kv_tokens, int max_seqlen_q, int max_seqlen_k, int num_heads,
+                                 int num_kv_heads, int head_dim, float softmax_scale, void* out,
+                                 int64_t out_tok_stride, int64_t out_head_stride,
+                                 void* workspace, int64_t workspace_bytes, void* stream, int dtype) {
   AttnParams P = {};
+  P.cache_dtype = dtype;  // the element type of q, k, v and out
   P.ws = workspace; P.ws_bytes = workspace_bytes;
   P.q = q; P.q_ts = q_tok_stride; P.q_hs = q_head_stride;
   P.k = k; P.v = v; P.k_ts = k_tok_stride; P.k_hs = k_head_stride;
@@ -305,6 +318,8 @@ extern "C" int nvs_varlen_attention(const void* q, int64_t q_tok_stride, int64_t
   if (rc != NVS_OK) return rc;
   NVS_REQUIRE(head_dim == kHeadDim, NVS_ERR_UNSUPPORTED,
               "varlen_attention: head_dim must be %d, got %d", kHeadDim, head_dim);
+  NVS_REQUIRE(dtype == NVS_DTYPE_BF16 || dtype == NVS_DTYPE_FP16, NVS_ERR_UNSUPPORTED,
+              "varlen_attention: dtype %d not served (bf16 / fp16)", dtype);
   NVS_REQUIRE(k && v, NVS_ERR_INVALID, "varlen_attention: null k/v pointer");
   NVS_REQUIRE(k_tok_stride % 8 == 0 && k_head_stride % 8 == 0 && v_tok_stride % 8 == 0 &&
                   v_head_stride % 8 == 0 && ((uintptr_t)k % 16) == 0 && ((uintptr_t)v % 16) == 0,
@@ -312,9 +327,44 @@ extern "C" int nvs_varlen_attention(const void* q, int64_t q_tok_stride, int64_t
   if (max_seqlen_q <= 0) return NVS_OK;
   rc = check_workspace(P, "varlen_attention");
   if (rc != NVS_OK) return rc;
+  rc = check_f16_served(P, "varlen_attention");
+  if (rc != NVS_OK) return rc;
   hipStream_t s = (hipStream_t)stream;
   const Plan plan = make_plan(workspace, P);
   rc = launch_plan(P, plan, /*paged=*/false, s);
   if (rc != NVS_OK) return rc;
   return launch_prefill_any(P, plan, s);
+}
+
+extern "C" int nvs_varlen_attention(const void* q, int64_t q_tok_stride, int64_t q_head_stride,
+                                    const void* k, const void* v, int64_t k_tok_stride,
+                                    int64_t k_head_stride, int64_t v_tok_stride,
+                                    int64_t v_head_stride, const int32_t* cu_seqlens_q,
+                                    const int32_t* cu_seqlens_k, int num_seqs, int64_t num_tokens,
+                                    int64_t num_kv_tokens, int max_seqlen_q, int max_seqlen_k, int num_heads,
+                                    int num_kv_heads, int head_dim, float softmax_scale, void* out,
+                                    int64_t out_tok_stride, int64_t out_head_stride,
+                                    void* workspace, int64_t workspace_bytes, void* stream) {
+  clear_error();
+  return varlen_attention_impl(q, q_tok_stride, q_head_stride, k, v, k_tok_stride, k_head_stride, v_tok_stride,
+                               v_head_stride, cu_seqlens_q, cu_seqlens_k, num_seqs, num_tokens, num_kv_tokens,
+                               max_seqlen_q, max_seqlen_k, num_heads, num_kv_heads, head_dim, softmax_scale, out,
+                               out_tok_stride, out_head_stride, workspace, workspace_bytes, stream,
+                               NVS_DTYPE_BF16);
+}
+
+extern "C" int nvs_varlen_attention_dtype(const void* q, int64_t q_tok_stride, int64_t q_head_stride,
+                                          const void* k, const void* v, int64_t k_tok_stride,
+                                          int64_t k_head_stride, int64_t v_tok_stride,
+                                          int64_t v_head_stride, const int32_t* cu_seqlens_q,
+                                          const int32_t* cu_seqlens_k, int num_seqs, int64_t num_tokens,
+                                          int64_t num_kv_tokens, int max_seqlen_q, int max_seqlen_k,
+                                          int num_heads, int num_kv_heads, int head_dim, float softmax_scale,
+                                          void* out, int64_t out_tok_stride, int64_t out_head_stride,
+                                          void* workspace, int64_t workspace_bytes, void* stream, int dtype) {
+  clear_error();
+  return varlen_attention_impl(q, q_tok_stride, q_head_stride, k, v, k_tok_stride, k_head_stride, v_tok_stride,
+                               v_head_stride, cu_seqlens_q, cu_seqlens_k, num_seqs, num_tokens, num_kv_tokens,
+                               max_seqlen_q, max_seqlen_k, num_heads, num_kv_heads, head_dim, softmax_scale, out,
+                               out_tok_stride, out_head_stride, workspace, workspace_bytes, stream, dtype);
 }

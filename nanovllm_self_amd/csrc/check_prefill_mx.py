@@ -64,7 +64,8 @@ def dests(ins: str):
 def parse_inc(path):
     text = open(path).read()
     blocks = {}
-    for name in ("NVS_PREFILL_MX_ASM_PAGED", "NVS_PREFILL_MX_ASM_LOCAL"):
+    for name in ("NVS_PREFILL_MX_ASM_PAGED", "NVS_PREFILL_MX_ASM_LOCAL", "NVS_PREFILL_MX_ASM_PAGED_F16",
+                 "NVS_PREFILL_MX_ASM_LOCAL_F16"):
         m = re.search(rf"#define {name} \\\n(.*?)\n  \"\"", text, re.S)
         lines = re.findall(r'"(.*?)\\n"', m.group(1))
         blocks[name] = lines

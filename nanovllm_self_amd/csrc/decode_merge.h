@@ -37,6 +37,7 @@ struct DecodeArgs {
   int64_t T;  // query / output rows
   uint16_t* out;
   int64_t out_ts, out_hs;
+  int f16;  // q and out are fp16 (an fp16 cache), else bf16
 };
 
 // First tile of decode group k of Kw over T tiles.
@@ -94,10 +95,17 @@ __device__ __forceinline__ void merge_split_row(const DecodeArgs& a, int unit, i
     if (use) {
       const float inv = L > 0.0f ? 1.0f / L : 0.0f;
       u32x4 v;
-      v[0] = pack_bf16x2(acc0[0] * inv, acc0[1] * inv);
-      v[1] = pack_bf16x2(acc0[2] * inv, acc0[3] * inv);
-      v[2] = pack_bf16x2(acc1[0] * inv, acc1[1] * inv);
-      v[3] = pack_bf16x2(acc1[2] * inv, acc1[3] * inv);
+      if (a.f16) {
+        v[0] = pack_f16x2(acc0[0] * inv, acc0[1] * inv);
+        v[1] = pack_f16x2(acc0[2] * inv, acc0[3] * inv);
+        v[2] = pack_f16x2(acc1[0] * inv, acc1[1] * inv);
+        v[3] = pack_f16x2(acc1[2] * inv, acc1[3] * inv);
+      } else {
+        v[0] = pack_bf16x2(acc0[0] * inv, acc0[1] * inv);
+        v[1] = pack_bf16x2(acc0[2] * inv, acc0[3] * inv);
+        v[2] = pack_bf16x2(acc1[0] * inv, acc1[1] * inv);
+        v[3] = pack_bf16x2(acc1[2] * inv, acc1[3] * inv);
+      }
       *reinterpret_cast<u32x4*>(a.out + (int64_t)q_row * a.out_ts + (int64_t)(h * a.g + c) * a.out_hs + 8 * j) = v;
     }
   }

@@ -2,8 +2,10 @@
 """Generator of the MFMA prefill kernel's persistent loop (paged_prefill_mx.hip)
 for gfx950.
 
-Writes prefill_mx_asm.inc next to this file: two string-literal macros
-(NVS_PREFILL_MX_ASM_PAGED, NVS_PREFILL_MX_ASM_LOCAL), each the body of one
+Writes prefill_mx_asm.inc next to this file: four string-literal macros
+(NVS_PREFILL_MX_ASM_PAGED, NVS_PREFILL_MX_ASM_LOCAL, and the _F16 pair for
+fp16 elements, which differ only in the MFMA, the packing instruction and
+the row-sum limit), each the body of one
 inline-asm statement that runs all of a work-group's prefill work: it claims
 units from its XCD's counter, decodes each from its plan record, and streams
 the units' 64-key tiles through one software pipeline that runs on from one
@@ -11,7 +13,7 @@ unit into the next.  Run it after editing this file:
 python nanovllm_self_amd/csrc/gen_prefill_mx.py
 
 Per wave: 64 query rows as two 32-row q-blocks (qb), one 64-key tile per
-iteration, v_mfma_f32_32x32x16_bf16 throughout:
+iteration, v_mfma_f32_32x32x16_bf16 (or _f16) throughout:
   S^T[kb][qb] (32 keys x 32 q)  = K . Q^T   16 d-steps x ... = 32 MFMAs
   O^T[n][qb]  (32 d x 32 q)    += V^T . P^T                   32 MFMAs
 Iteration j: segment A runs PV of tile j-1 beside the first exponentials of
@@ -26,7 +28,7 @@ unit u+1's key tiles 0 and 1; u's last iteration reads u+1's query rows (in
 the wave's query stage since u began) into the Q^T registers and runs QK^T of
 u+1's tile 0 in its segment B; u+1's first iteration runs the PV of u's last
 tile in its segment A and, beside the QK^T of its tile 1, normalises u's
-output and stores it as bf16 rows straight from registers
+output and stores it as bf16 (fp16) rows through the wave's query stage
 (v_permlane32_swap_b32 pairs the lane halves' 8-byte pieces into 16-byte
 chunks).  The iteration parity runs on across units, so u's last V tile and
 u+1's first tiles are in opposite buffers.  A unit of one tile, a unit
@@ -67,7 +69,19 @@ from __future__ import annotations
 import os
 import sys
 
+# The element type of Q, K, V, P and the output: bf16, or fp16 (an fp16
+# cache).  set_element() switches the MFMA, the packing of P and of the
+# output, and the row-sum limit.
 MF = "v_mfma_f32_32x32x16_bf16"
+CVT = "v_cvt_pk_bf16_f32"
+
+
+def set_element(f16):
+    global MF, CVT, SUM_LIMIT
+    MF = "v_mfma_f32_32x32x16_f16" if f16 else "v_mfma_f32_32x32x16_bf16"
+    CVT = "v_cvt_pk_f16_f32" if f16 else "v_cvt_pk_bf16_f32"
+    SUM_LIMIT = SUM_LIMIT_F16 if f16 else SUM_LIMIT_BF16
+
 
 # ----------------------------------------------------------- register map
 def S(par, kb, qb):
@@ -247,8 +261,11 @@ class Emitter:
 
 # ------------------------------------------------------------- VALU lists
 # the row sums of a tile may reach SUM_LIMIT before the running max moves:
-# no exponential of a tile exceeds 2^16 times the row's running max term
-SUM_LIMIT = "0x47800000"  # 65536.0
+# no exponential of a tile exceeds 2^16 times the row's running max term.
+# fp16 P holds at most 65504: its limit is 2^15.
+SUM_LIMIT_BF16 = "0x47800000"  # 65536.0
+SUM_LIMIT_F16 = "0x47000000"  # 32768.0
+SUM_LIMIT = SUM_LIMIT_BF16
 
 
 def row_max(par):
@@ -350,7 +367,7 @@ def exp_items(pairs, k0, touched):
             it.append(f"v_exp_f32 {t[k][0]}, {t[k][0]}")
             it.append(f"v_exp_f32 {t[k][1]}, {t[k][1]}")
         for k, (_, a, b, p) in enumerate(grp):
-            it.append(f"v_cvt_pk_bf16_f32 {p}, {t[k][0]}, {t[k][1]}")
+            it.append(f"{CVT} {p}, {t[k][0]}, {t[k][1]}")
         # t0 + t1 -> t0, t2 + t3 -> t2, ... then two partial sums
         for k in range(len(grp)):
             it.append(f"v_add_f32 {t[k][0]}, {t[k][0]}, {t[k][1]}")
@@ -938,7 +955,7 @@ def output_items(bank, lsum, tmp, zero_o, qnext=False):
                 g = groups[gi % len(groups)]
                 gi += 1
                 for e in range(4):
-                    it.append(f"v_cvt_pk_bf16_f32 v{g + e}, {tv[2 * e]}, {tv[2 * e + 1]}")
+                    it.append(f"{CVT} v{g + e}, {tv[2 * e]}, {tv[2 * e + 1]}")
                 it.append("s_nop 1")
                 it.append(f"v_permlane32_swap_b32 v{g}, v{g + 2}")
                 it.append(f"v_permlane32_swap_b32 v{g + 1}, v{g + 3}")
@@ -1429,6 +1446,10 @@ def main():
     here = os.path.dirname(os.path.abspath(__file__))
     paged = program(True)
     local = program(False)
+    set_element(True)
+    paged16 = program(True)
+    local16 = program(False)
+    set_element(False)
     clob = ", ".join(f'"{c}"' for c in CLOBBERS)
     text = [
         "// Generated by gen_prefill_mx.py; do not edit by hand.",
@@ -1439,13 +1460,17 @@ def main():
         "",
         render("NVS_PREFILL_MX_ASM_LOCAL", local),
         "",
+        render("NVS_PREFILL_MX_ASM_PAGED_F16", paged16),
+        "",
+        render("NVS_PREFILL_MX_ASM_LOCAL_F16", local16),
+        "",
         f"#define NVS_PREFILL_MX_CLOBBERS {clob}",
         "",
     ]
     path = os.path.join(here, "prefill_mx_asm.inc")
     with open(path, "w") as f:
         f.write("\n".join(text))
-    print(f"wrote {path}: {len(paged)} + {len(local)} lines", file=sys.stderr)
+    print(f"wrote {path}: {len(paged)} + {len(local)} lines (and as many for fp16)", file=sys.stderr)
 
 
 if __name__ == "__main__":

@@ -71,6 +71,13 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
 }
 
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// Two fp32 -> packed fp16x2 (low half = a), RNE.
+__device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, f16x2));
+}
+
 // acc + lo(x) + hi(x) for a packed bf16x2 x, in fp32 (v_dot2c_f32_bf16 with 1.0).
 __device__ __forceinline__ float add_bf16x2(uint32_t x, float acc) {
   const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};

@@ -46,6 +46,29 @@
 namespace nvs {
 
 
+// Caches of 16-bit values (bf16, fp16) share the tile layout and loads; the
+// MFMA and the packing of P and of the output follow the element type.
+// Code caches compute in bf16.
+template <int KV>
+constexpr bool kHalf = KV == NVS_DTYPE_BF16 || KV == NVS_DTYPE_FP16;
+
+template <int KV>
+__device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
+  if constexpr (KV == NVS_DTYPE_FP16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
+                                                  0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+template <int KV>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  if constexpr (KV == NVS_DTYPE_FP16)
+    return pack_f16x2(a, b);
+  else
+    return pack_bf16x2(a, b);
+}
+
 // Registers of one 32-key tile as loaded from HBM.  `has` is false when the
 // tile's block-table entry is missing (< 0 or outside the pool); the loads
 // then read block 0 and the compute treats the keys as zero vectors.
@@ -58,6 +81,9 @@ struct DecodeTile<NVS_DTYPE_BF16> {
   u32x4 v[8];     // [slot e]: key 16(e/4) + 4 grp + e%4, d = 8 col .. +7
   bool has;
 };
+
+template <>
+struct DecodeTile<NVS_DTYPE_FP16> : DecodeTile<NVS_DTYPE_BF16> {};
 
 template <int KV>
 struct DecodeTile {
@@ -75,9 +101,9 @@ __device__ __forceinline__ int slot_key(int e, int grp) { return 16 * (e >> 2) +
 // instruction reads 64 contiguous bytes of each of its 16 rows, code caches
 // keep d = 32 grp + 8 s (one 128-byte row per lane group pair of loads).
 template <int KV>
-constexpr int kKStepStride = (KV == NVS_DTYPE_BF16) ? 32 : 8;
+constexpr int kKStepStride = kHalf<KV> ? 32 : 8;
 template <int KV>
-constexpr int kKGroupStride = (KV == NVS_DTYPE_BF16) ? 8 : 32;
+constexpr int kKGroupStride = kHalf<KV> ? 8 : 32;
 
 // Per-lane byte offsets from a tile's first row, identical for every tile.
 // A load of slot e adds the wave-uniform offset of key row slot_key(e, 0)
@@ -89,7 +115,7 @@ struct LaneOffsets {
 
 template <int KV>
 __device__ __forceinline__ LaneOffsets lane_offsets(int Hkv, int col, int grp) {
-  constexpr uint32_t ESZ = (KV == NVS_DTYPE_BF16) ? 2 : 1;
+  constexpr uint32_t ESZ = kHalf<KV> ? 2 : 1;
   const uint32_t row = (uint32_t)Hkv * kHeadDim * ESZ;  // bytes per token row (all heads)
   LaneOffsets o;
   o.k = (uint32_t)col * row + kKGroupStride<KV> * grp * ESZ;
@@ -120,14 +146,14 @@ __device__ __forceinline__ T v_load(const T* p) {
 template <int KV>
 __device__ __forceinline__ void decode_load(DecodeTile<KV>& T, const DecodeArgs& a, const LaneOffsets& lo,
                                             int blk, int koff, int h) {
-  constexpr int ESZ = (KV == NVS_DTYPE_BF16) ? 2 : 1;
+  constexpr int ESZ = kHalf<KV> ? 2 : 1;
   T.has = blk >= 0;
   const int64_t row0 = ((int64_t)(T.has ? blk : 0) * a.bs + koff) * a.Hkv + h;
   const int64_t rowb = (int64_t)a.Hkv * kHeadDim * ESZ;  // bytes per token row
   const char* kb = (const char*)a.kc + row0 * kHeadDim * ESZ;
   const char* vb = (const char*)a.vc + row0 * kHeadDim * ESZ;
   const uint32_t ok = lane_off(lo.k), ov = lane_off(lo.v);
-  if constexpr (KV == NVS_DTYPE_BF16) {
+  if constexpr (kHalf<KV>) {
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -158,7 +184,7 @@ __device__ __forceinline__ void decode_load(DecodeTile<KV>& T, const DecodeArgs&
 // (the loads fetched block 0).
 template <int KV>
 __device__ __forceinline__ void zero_tile(DecodeTile<KV>& T) {
-  if constexpr (KV == NVS_DTYPE_BF16) {
+  if constexpr (kHalf<KV>) {
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -231,20 +257,20 @@ __device__ __forceinline__ void decode_tile_compute(const DecodeTile<KV>& T, con
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
       bf16x8 kop;
-      if constexpr (KV == NVS_DTYPE_BF16) {
+      if constexpr (kHalf<KV>) {
         kop = __builtin_bit_cast(bf16x8, T.k[t][st]);
       } else {
         const u32x4 w = T.k[t][st >> 1];
         kop = codes8_to_bf16x8<KV>(w[2 * (st & 1)], w[2 * (st & 1) + 1]);
       }
-      s[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qop[st], s[t], 0, 0, 0);
+      s[t] = mfma16x16x32<KV>(kop, qop[st], s[t]);
     }
   }
   // ---- per-key scales of quantised caches: slot e of this lane is key
   // slot_key(e, grp), whose k scale lane slot_key(e, grp) holds and whose v
   // scale lane 32 + slot_key(e, grp) holds.
   float ksc[8], vsc[8];
-  if constexpr (KV != NVS_DTYPE_BF16) tile_scales(T.sc, grp, ksc, vsc);
+  if constexpr (!kHalf<KV>) tile_scales(T.sc, grp, ksc, vsc);
   // ---- online softmax (log2 domain) -----------------------------------------
   bool valid[8];
 #pragma unroll
@@ -253,7 +279,7 @@ __device__ __forceinline__ void decode_tile_compute(const DecodeTile<KV>& T, con
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     float f = scale_log2;
-    if constexpr (KV != NVS_DTYPE_BF16) f *= ksc[e];
+    if constexpr (!kHalf<KV>) f *= ksc[e];
     float x = s[e >> 2][e & 3] * f;
     if constexpr (MASKED) x = valid[e] ? x : -INFINITY;  // outside the partition
     sv[e] = x;
@@ -277,13 +303,13 @@ __device__ __forceinline__ void decode_tile_compute(const DecodeTile<KV>& T, con
     const float p = fast_exp2(sv[e] - m_run);
     l_run += p;
     float pw = p;
-    if constexpr (KV != NVS_DTYPE_BF16) pw = p * vsc[e];
+    if constexpr (!kHalf<KV>) pw = p * vsc[e];
     if constexpr (MASKED) pw = valid[e] ? pw : 0.0f;
     pv[e] = pw;
   }
   u32x4 pw;
 #pragma unroll
-  for (int m = 0; m < 4; ++m) pw[m] = pack_bf16x2(pv[2 * m], pv[2 * m + 1]);
+  for (int m = 0; m < 4; ++m) pw[m] = pack2<KV>(pv[2 * m], pv[2 * m + 1]);
   const bf16x8 pop = __builtin_bit_cast(bf16x8, pw);
 
   // ---- V^T operands (transpose in registers) and O^T += V^T . P^T ---------
@@ -291,12 +317,12 @@ __device__ __forceinline__ void decode_tile_compute(const DecodeTile<KV>& T, con
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
     const bool v0 = valid[2 * m], v1 = valid[2 * m + 1];
-    if constexpr (KV == NVS_DTYPE_BF16)
+    if constexpr (kHalf<KV>)
       keep[m] = (v0 ? 0x0000ffffu : 0u) | (v1 ? 0xffff0000u : 0u);
     else
       keep[m] = (v0 ? 0x00ff00ffu : 0u) | (v1 ? 0xff00ff00u : 0u);
   }
-  if constexpr (KV == NVS_DTYPE_BF16) {
+  if constexpr (kHalf<KV>) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
@@ -305,8 +331,7 @@ __device__ __forceinline__ void decode_tile_compute(const DecodeTile<KV>& T, con
       for (int m = 0; m < 4; ++m)
         aw[m] = __builtin_amdgcn_perm(T.v[2 * m + 1][j >> 1], T.v[2 * m][j >> 1],
                                       MASKED ? masked_sel(sel, keep[m]) : sel);
-      o[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, aw), pop, o[j], 0,
-                                                     0, 0);
+      o[j] = mfma16x16x32<KV>(__builtin_bit_cast(bf16x8, aw), pop, o[j]);
     }
   } else {
 #pragma unroll
@@ -456,6 +481,11 @@ __device__ __forceinline__ void store_new_token(const DecodeArgs& a, int q0, int
   if constexpr (KV == NVS_DTYPE_BF16) {
     char* dst = (char*)(isv ? a.vc : a.kc) + row * (int64_t)(kHeadDim * 2);
     *reinterpret_cast<u32x4*>(dst + off) = *reinterpret_cast<const u32x4*>(src + off);
+  } else if constexpr (KV == NVS_DTYPE_FP16) {  // bf16 sources cast to fp16 (RNE)
+    float x[8];
+    load8<NVS_DTYPE_BF16>(src + off, x);
+    char* dst = (char*)(isv ? a.vc : a.kc) + row * (int64_t)(kHeadDim * 2);
+    store8_float<NVS_DTYPE_FP16>(dst + off, x);
   } else {
     float x[8];
     load8<NVS_DTYPE_BF16>(src + off, x);
@@ -713,7 +743,9 @@ __device__ __forceinline__ void finish_segment(const DecodeArgs& a, const Cursor
     for (int r = 0; r < 4; ++r) {
       u32x4 v;
 #pragma unroll
-      for (int m = 0; m < 4; ++m) v[m] = pack_bf16x2(o[2 * m][r] * inv, o[2 * m + 1][r] * inv);
+      for (int m = 0; m < 4; ++m)
+        v[m] = a.f16 ? pack_f16x2(o[2 * m][r] * inv, o[2 * m + 1][r] * inv)
+                     : pack_bf16x2(o[2 * m][r] * inv, o[2 * m + 1][r] * inv);
       *reinterpret_cast<u32x4*>(ob + lo + 16 * r) = v;
     }
   } else {
@@ -743,7 +775,7 @@ __device__ __forceinline__ void finish_segment(const DecodeArgs& a, const Cursor
 #define NVS_DECODE_RING_CODES 2
 #endif
 template <int KV>
-constexpr int kDecodeRing = (KV == NVS_DTYPE_BF16) ? NVS_DECODE_RING_BF16 : NVS_DECODE_RING_CODES;
+constexpr int kDecodeRing = kHalf<KV> ? NVS_DECODE_RING_BF16 : NVS_DECODE_RING_CODES;
 
 // Decode ranges: Kw groups of Hkv waves (one per kv head) share the T tiles,
 // group k taking [floor(k T / Kw), floor((k + 1) T / Kw)); Kw = min(launched
@@ -948,6 +980,7 @@ int launch_decode(const AttnParams& P, int max_waves, int waves, void* partials,
   a.kn_ts = P.kn_ts; a.kn_hs = P.kn_hs; a.vn_ts = P.vn_ts; a.vn_hs = P.vn_hs;
   a.slots = P.slots; a.total_slots = P.NB * (int64_t)P.bs;
   a.out = (uint16_t*)P.out; a.out_ts = P.out_ts; a.out_hs = P.out_hs;
+  a.f16 = P.cache_dtype == NVS_DTYPE_FP16 ? 1 : 0;
   a.ws_o = (float*)partials;
   a.ws_ml = a.ws_o + (int64_t)max_waves * 2 * a.g * kHeadDim;
   a.ws_rec = (int32_t*)(a.ws_ml + (int64_t)max_waves * 2 * a.g * 2);
@@ -956,6 +989,9 @@ int launch_decode(const AttnParams& P, int max_waves, int waves, void* partials,
   switch (P.cache_dtype) {
     case NVS_DTYPE_BF16:
       hipLaunchKernelGGL(paged_decode_kernel<NVS_DTYPE_BF16>, grid, block, 0, stream, a, P.bt, P.cu_q, P.cu_k);
+      break;
+    case NVS_DTYPE_FP16:
+      hipLaunchKernelGGL(paged_decode_kernel<NVS_DTYPE_FP16>, grid, block, 0, stream, a, P.bt, P.cu_q, P.cu_k);
       break;
     case NVS_DTYPE_INT8:
       hipLaunchKernelGGL(paged_decode_kernel<NVS_DTYPE_INT8>, grid, block, 0, stream, a, P.bt, P.cu_q, P.cu_k);

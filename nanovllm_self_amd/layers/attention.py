@@ -25,8 +25,8 @@ import torch.nn as nn
 from .. import _lib
 from ..utils.context import Context
 
-_COMPUTE_DTYPES = (torch.bfloat16,)
-_SERVED_CACHE_DTYPES = (torch.bfloat16, torch.int8, torch.float8_e4m3fn)
+_COMPUTE_DTYPES = (torch.bfloat16, torch.float16)
+_SERVED_CACHE_DTYPES = (torch.bfloat16, torch.float16, torch.int8, torch.float8_e4m3fn)
 _QUANT_DTYPE = {"int8_mock": torch.int8, "fp8_e4m3": torch.float8_e4m3fn}
 
 _workspaces: dict = {}
@@ -262,19 +262,33 @@ class PagedAttention(nn.Module):
         """One call of the HIP attention over the whole (mixed) batch; with
         store_slots the same call first writes k / v to those cache slots
         (nvs_paged_attention_store, paged mode only)."""
-        compute = torch.bfloat16
-        # These kernels compute in bf16, the reference's default
-        # attention_compute_dtype (config.py:33-38).  A layer set to compute
-        # in another dtype (fp16: attention.py:22-23, 327-330; fp32 through
-        # the eager path) is refused in both modes rather than computed in
-        # bf16.  q / k / v of another dtype are cast to the compute dtype, as
-        # the reference casts them (attention.py:340-342, 362).
-        if self.attention_compute_dtype != compute:
-            name = {torch.float16: "fp16", torch.float32: "fp32"}.get(self.attention_compute_dtype,
-                                                                      str(self.attention_compute_dtype))
+        # The kernels compute in bf16 or fp16 (attention_compute_dtype,
+        # config.py:33-38; the reference's flash path computes in it,
+        # attention.py:326-336): the local mode in attention_compute_dtype,
+        # the paged mode in the dtype of a bf16 / fp16 cache, and in bf16 over
+        # int8 / fp8 codes.  fp32 attention (the eager path's) is refused in
+        # both modes, and so are codes with fp16 compute (the reference
+        # dequantises them to fp16 there; these kernels to bf16).  q / k / v
+        # of another dtype are cast to the element type, as the reference
+        # casts them (attention.py:340-342, 362).
+        paged = context.block_tables is not None
+        if self.attention_compute_dtype not in _COMPUTE_DTYPES:
+            name = {torch.float32: "fp32"}.get(self.attention_compute_dtype, str(self.attention_compute_dtype))
             raise RuntimeError(
-                f"HIP attention computes in bf16: {name} attention (attention_compute_dtype "
+                f"HIP attention computes in bf16 or fp16: {name} attention (attention_compute_dtype "
                 f"{self.attention_compute_dtype}) is not served")
+        if not paged:
+            compute = self.attention_compute_dtype
+        elif self.k_cache is None or self.v_cache is None:
+            raise RuntimeError("k_cache / v_cache are not bound")
+        elif self.k_cache.dtype in (torch.bfloat16, torch.float16):
+            compute = self.k_cache.dtype
+        else:
+            compute = torch.bfloat16
+            if self.attention_compute_dtype != torch.bfloat16:
+                raise RuntimeError(
+                    f"HIP attention over int8 / fp8 codes computes in bf16: attention_compute_dtype "
+                    f"{self.attention_compute_dtype} is not served with a {self.k_cache.dtype} cache")
         if q.dtype != compute:
             q = q.to(compute)
         _need_device(q, "q")
@@ -308,19 +322,20 @@ class PagedAttention(nn.Module):
             if v.stride(-1) != 1:
                 v = v.contiguous()
             _lib.check(
-                lib.nvs_varlen_attention(
+                lib.nvs_varlen_attention_dtype(
                     q.data_ptr(), q.stride(0), q.stride(1),
                     k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1), v.stride(0), v.stride(1),
                     cu_q.data_ptr(), cu_k.data_ptr(), B, T, k.shape[0], max_q, max_k,
                     self.num_heads, self.num_kv_heads, self.head_dim, scale,
                     out.data_ptr(), out.stride(0), out.stride(1), _lib.ptr(ws), ws_bytes, stream,
+                    _lib.nvs_dtype(compute),
                 ),
                 "varlen_attention",
             )
         else:
             kc, vc = self.k_cache, self.v_cache
             if kc.dtype not in _SERVED_CACHE_DTYPES:
-                raise RuntimeError(f"HIP attention serves bf16/int8/fp8 KV caches, got {kc.dtype}")
+                raise RuntimeError(f"HIP attention serves bf16/fp16/int8/fp8 KV caches, got {kc.dtype}")
             mode = self.kv_cache_quant_mode
             quant = kc.dtype in (torch.int8, torch.float8_e4m3fn)
             if quant and mode not in _QUANT_DTYPE:

@@ -34,7 +34,7 @@ from .kv_cache import KVCacheConfig, SeqSlice, allocate_kv_cache, bind_kv_cache,
 from .layers.attention import PagedAttention
 from .utils.context import Context
 
-QUANT_MODE = {"bf16": "none", "int8": "int8_mock", "fp8": "fp8_e4m3"}
+QUANT_MODE = {"bf16": "none", "fp16": "none", "int8": "int8_mock", "fp8": "fp8_e4m3"}
 
 
 @dataclass
@@ -45,7 +45,7 @@ class Workload:
     head_dim: int
     block_size: int
     num_blocks: int
-    kv: str  # "bf16" | "int8" | "fp8"
+    kv: str  # "bf16" | "fp16" (an fp16 model: fp16 cache and compute) | "int8" | "fp8"
     attn: PagedAttention
     q: torch.Tensor
     k: torch.Tensor
@@ -69,8 +69,8 @@ class Workload:
     def decode_bytes(self) -> int:
         """Algorithmic HBM bytes of the decode rows: every visible K/V element
         (and scale) once, plus q read and o written."""
-        s_kv = 2 if self.kv == "bf16" else 1
-        s_sc = 0 if self.kv == "bf16" else 4
+        s_kv = 2 if self.kv in ("bf16", "fp16") else 1
+        s_sc = 0 if self.kv in ("bf16", "fp16") else 4
         ctx = sum(self.seqs[i].num_cached_tokens + 1 for i in self.decode_seq_ids())
         nd = len(self.decode_seq_ids())
         H, Hq, D = self.num_kv_heads, self.num_heads, self.head_dim
@@ -93,12 +93,12 @@ def _gen(seed: int) -> torch.Generator:
     return g
 
 
-def _randn(g, shape, scale=1.0, outliers=False):
+def _randn(g, shape, scale=1.0, outliers=False, dtype=torch.bfloat16):
     x = torch.randn(shape, generator=g, dtype=torch.float32) * scale
     if outliers:
         hit = torch.rand(shape, generator=g) < 0.01
         x = torch.where(hit, x * 8.0, x)
-    return x.to(torch.bfloat16)
+    return x.to(dtype)
 
 
 def _fill_history(wl: Workload, seed: int, k_scale: float, outliers: bool) -> None:
@@ -129,23 +129,25 @@ def _fill_history(wl: Workload, seed: int, k_scale: float, outliers: bool) -> No
         if outliers:
             kk = torch.where(torch.rand(kk.shape, generator=g, device=dev) < 0.01, kk * 8.0, kk)
             vv = torch.where(torch.rand(vv.shape, generator=g, device=dev) < 0.01, vv * 8.0, vv)
-        wl.attn.store_kv_cache_torch(kk.to(torch.bfloat16), vv.to(torch.bfloat16), sl)
+        src = torch.float16 if wl.kv == "fp16" else torch.bfloat16
+        wl.attn.store_kv_cache_torch(kk.to(src), vv.to(src), sl)
 
 
 def _assemble(name, seqs, Hq, Hkv, D, bs, NB, kv, device, g, k_scale=1.0, outliers=False,
               seed=0) -> Workload:
+    elem = torch.float16 if kv == "fp16" else torch.bfloat16
     cfg = KVCacheConfig(
-        dtype=torch.bfloat16, kv_cache_dtype=torch.bfloat16,
-        attention_compute_dtype=torch.bfloat16, kv_cache_quant_mode=QUANT_MODE[kv],
+        dtype=elem, kv_cache_dtype=elem,
+        attention_compute_dtype=elem, kv_cache_quant_mode=QUANT_MODE[kv],
         block_size=bs, num_blocks=NB,
     )
-    attn = PagedAttention(Hq, Hkv, D, dtype=torch.bfloat16)
+    attn = PagedAttention(Hq, Hkv, D, dtype=elem)
     kv_cache, kv_scale_cache = allocate_kv_cache(1, Hkv, D, cfg, device)
     bind_kv_cache([attn], kv_cache, kv_scale_cache, cfg)
     T = sum(s.num_new_tokens for s in seqs)
-    q = _randn(g, (T, Hq, D)).to(device)
-    k = _randn(g, (T, Hkv, D), k_scale, outliers).to(device)
-    v = _randn(g, (T, Hkv, D), 1.0, outliers).to(device)
+    q = _randn(g, (T, Hq, D), dtype=elem).to(device)
+    k = _randn(g, (T, Hkv, D), k_scale, outliers, dtype=elem).to(device)
+    v = _randn(g, (T, Hkv, D), 1.0, outliers, dtype=elem).to(device)
     ctx = build_context(seqs, bs, device)
     wl = Workload(name, Hq, Hkv, D, bs, NB, kv, attn, q, k, v, ctx, list(seqs), kv_cache, kv_scale_cache)
     _fill_history(wl, seed, k_scale, outliers)

@@ -30,18 +30,21 @@ def say(*args):
 
 
 def bf16_to_np(t: torch.Tensor) -> np.ndarray:
+    """float32 copy of a bf16 (or fp16) tensor, exact."""
+    if t.dtype == torch.float16:
+        return t.detach().cpu().float().numpy()
     return KO.bf16_bits_to_f32(t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16))
 
 
 def cache_blocks_f32(attn, blocks: np.ndarray):
     """Dequantised float32 copies of the given cache blocks, as the eager
-    path sees them: bf16 caches as stored; int8 / fp8 codes * scale rounded
+    path sees them: bf16 / fp16 caches as stored; int8 / fp8 codes * scale rounded
     to bf16 (dequantize_int8_per_token's .to(attention_compute_dtype))."""
     idx = torch.as_tensor(blocks, dtype=torch.long, device=attn.k_cache.device)
     out = []
     for cache, scale in ((attn.k_cache, attn.k_scale_cache), (attn.v_cache, attn.v_scale_cache)):
         sub = cache.index_select(0, idx).cpu()
-        if sub.dtype == torch.bfloat16:
+        if sub.dtype in (torch.bfloat16, torch.float16):
             out.append(bf16_to_np(sub))
             continue
         codes = sub.view(torch.uint8).numpy()

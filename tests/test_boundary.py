@@ -158,9 +158,10 @@ def test_dtype_mismatch_guard():
 
 
 @pytest.mark.parametrize("paged", [False, True])
-def test_fp16_attention_is_refused_in_both_modes(paged):
-    """fp16 compute is not served: local mode (block_tables None) and paged
-    mode both raise instead of rounding q/k/v to bf16."""
+def test_fp16_attention_reaches_the_kernels(paged):
+    """fp16 compute is served in both modes (the reference's flash path
+    computes in fp16, attention.py:326-336): with CPU tensors the call gets
+    past the dtype checks and stops at the device check."""
     a = PagedAttention(8, 8, 128)
     a.block_size = 256
     a.k_cache = torch.zeros(1, 256, 8, 128, dtype=torch.float16)
@@ -170,8 +171,28 @@ def test_fp16_attention_is_refused_in_both_modes(paged):
     cu = torch.tensor([0, 1], dtype=torch.int32)
     ctx = Context(cu_seqlens_q=cu, cu_seqlens_k=cu, max_seqlen_q=1, max_seqlen_k=1,
                   block_tables=torch.zeros(1, 1, dtype=torch.int32) if paged else None)
-    with pytest.raises(RuntimeError, match="fp16 attention"):
+    with pytest.raises(RuntimeError, match="GPU tensor"):
         a.prefill_flashattn(z, z, z, ctx)
+
+
+def test_fp16_compute_over_codes_is_refused():
+    """int8 / fp8 codes are dequantised to bf16 by these kernels, where the
+    reference's eager path would round them to an fp16 compute dtype: the
+    layer refuses that combination instead of computing in bf16."""
+    a = PagedAttention(8, 8, 128)
+    a.block_size = 256
+    a.kv_cache_quant_mode = "int8_mock"
+    a.k_cache = torch.zeros(1, 256, 8, 128, dtype=torch.int8)
+    a.v_cache = torch.zeros_like(a.k_cache)
+    a.k_scale_cache = torch.ones(1, 256, 8, 1)
+    a.v_scale_cache = torch.ones(1, 256, 8, 1)
+    a.attention_compute_dtype = torch.float16
+    z = torch.zeros(1, 8, 128, dtype=torch.float16)
+    cu = torch.tensor([0, 1], dtype=torch.int32)
+    ctx = Context(cu_seqlens_q=cu, cu_seqlens_k=cu, max_seqlen_q=1, max_seqlen_k=1,
+                  block_tables=torch.zeros(1, 1, dtype=torch.int32))
+    with pytest.raises(RuntimeError, match="codes computes in bf16"):
+        a.prefill_torch(z, z, z, ctx)
 
 
 @pytest.mark.parametrize("paged", [False, True])
