@@ -72,10 +72,13 @@ static Plan make_plan(void* ws, const AttnParams& P) {
 }
 
 // fp16 elements run only on the tile-loop kernel (the classic kernel is
-// bf16 and code caches); a call it does not serve is refused before any
-// launch.
+// bf16 and code caches); a call with prefill work it does not serve is
+// refused before any launch.  Paged calls have prefill work when
+// max_seqlen_q > 1 (q_len == 1 rows go to the decode kernel), local calls
+// always.
 static int check_f16_served(const AttnParams& P, const char* who) {
-  NVS_REQUIRE(P.cache_dtype != NVS_DTYPE_FP16 || P.max_seqlen_q <= 1 || prefill_mx_serves(P),
+  const bool prefill = P.bt ? P.max_seqlen_q > 1 : P.max_seqlen_q > 0;
+  NVS_REQUIRE(P.cache_dtype != NVS_DTYPE_FP16 || !prefill || prefill_mx_serves(P),
               NVS_ERR_UNSUPPORTED,
               "%s: fp16 prefill runs on the tile-loop kernel only, which does not serve this call "
               "(NVS_PREFILL_KERNEL=classic, or strides past its 32-bit lane offsets)", who);

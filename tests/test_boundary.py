@@ -262,6 +262,23 @@ def test_c_abi_validates_before_launch():
     assert lib.nvs_store_kvcache(P, P, 0, 8, 8, 8, 8, P, 0, P, P, 0, None, None, 8, 256, 8, 128, None) == 0
 
 
+def test_fp16_calls_the_tile_loop_cannot_serve_are_refused():
+    """fp16 prefill runs on the tile-loop kernel only: a local-mode fp16 call
+    whose k and v token strides differ (which that kernel does not serve) is
+    refused on the host, where a bf16 call would go to the classic kernel;
+    the same strides in bf16 get past the check to the launch (which the
+    fake pointers never reach: the dtype is refused first)."""
+    lib = _lib.load()
+    P = 1 << 20  # 16-byte aligned, never touched
+    ws = 1 << 21
+    args = (P, 1024, 128, P, P, 1024, 128, 2048, 128, P, P, 1, 4, 4, 4, 4, 8, 8, 128, 0.088,
+            P, 1024, 128, ws, 1 << 24, None)
+    rc = lib.nvs_varlen_attention_dtype(*args, 1)
+    assert rc == -2 and b"tile-loop" in lib.nvs_last_error()
+    rc = lib.nvs_varlen_attention_dtype(*args, 2)
+    assert rc == -2 and b"dtype" in lib.nvs_last_error()
+
+
 def test_workspace_bytes():
     """The prefill plan (256-byte header + prefill list + a 64-byte record
     per list entry, each 256-aligned) followed by the decode partials: two slots of g x (128 + 2) floats per decode
