@@ -61,3 +61,29 @@ def test_random_batch_matches_oracle(device, seed):
         return
     ref, rows = oracle_paged(wl, list(range(len(spec))))
     compare(got[rows], ref, kv != "bf16", f"random batch {seed}")
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_fp16_batch_matches_oracle(device, seed):
+    """The same draws (other seeds) with an fp16 model: fp16 q / k / v and
+    cache, fp16 compute and output."""
+    Hkv, g, bs, _, spec = _draw(100 + seed)
+    say(f"random fp16 batch {seed}: Hkv={Hkv} g={g} block_size={bs} rows (cached, new)={spec}")
+    lens = [p + n for p, n in spec]
+    NB = sum((n + bs - 1) // bs for n in lens) + 2
+    gen = torch.Generator().manual_seed(100 + seed)
+    tabs = W._tables(gen, lens, bs, NB)
+    seqs = [SeqSlice(tabs[i], p, n) for i, (p, n) in enumerate(spec)]
+    wl = W._assemble("random-fp16", seqs, g * Hkv, Hkv, 128, bs, NB, "fp16", device, gen, seed=100 + seed)
+    out = wl.attn.forward(wl.q, wl.k, wl.v, wl.context)
+    torch.cuda.synchronize()
+    assert out.dtype == torch.float16
+    got = bf16_to_np(out)
+    if wl.context.block_tables is None:
+        ref = AO.attention_local(torch.from_numpy(bf16_to_np(wl.q)), torch.from_numpy(bf16_to_np(wl.k)),
+                                 torch.from_numpy(bf16_to_np(wl.v)), wl.context.cu_seqlens_q.cpu(),
+                                 g * Hkv, Hkv, 128)
+        compare(got, ref.numpy(), False, f"random fp16 batch {seed} (local)")
+        return
+    ref, rows = oracle_paged(wl, list(range(len(spec))))
+    compare(got[rows], ref, False, f"random fp16 batch {seed}")
