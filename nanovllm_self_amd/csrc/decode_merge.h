@@ -43,15 +43,85 @@ struct DecodeArgs {
 // First tile of decode group k of Kw over T tiles.
 __device__ __forceinline__ int group_start(int T, int Kw, int k) { return (int)((int64_t)k * T / Kw); }
 
+// Heads c0 + lane / 16 + 4 i (i < NH) of the row: NH head passes at once,
+// so a group of more than four heads waits for its partials' loads once
+// rather than once per four heads.
+template <int NH>
+__device__ __forceinline__ void merge_heads(const DecodeArgs& a, int h, int k, int k_last, int slot_k, int q_row,
+                                            int c0, int lane) {
+  const int j = lane & 15;
+  int cc[NH];
+  bool use[NH];
+  float M[NH], L[NH];
+  f32x4 acc0[NH], acc1[NH];
+#pragma unroll
+  for (int i = 0; i < NH; ++i) {
+    const int c = c0 + (lane >> 4) + 4 * i;
+    use[i] = c < a.g;
+    cc[i] = use[i] ? c : 0;
+    M[i] = -INFINITY;
+    L[i] = 0.0f;
+    acc0[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    acc1[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  for (int x0 = k; x0 <= k_last; x0 += 4) {
+    f32x2 ml[4][NH];
+    f32x4 o0[4][NH], o1[4][NH];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int x = min(x0 + u, k_last);
+#pragma unroll
+      for (int i = 0; i < NH; ++i) {
+        const int64_t base = (((int64_t)x * a.Hkv + h) * 2 + (x == k ? slot_k : 0)) * a.g + cc[i];
+        ml[u][i] = *reinterpret_cast<const f32x2*>(a.ws_ml + base * 2);
+        o0[u][i] = *reinterpret_cast<const f32x4*>(a.ws_o + base * kHeadDim + 8 * j);
+        o1[u][i] = *reinterpret_cast<const f32x4*>(a.ws_o + base * kHeadDim + 8 * j + 4);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if (x0 + u > k_last) break;
+#pragma unroll
+      for (int i = 0; i < NH; ++i) {
+        const float m_new = fmaxf(M[i], ml[u][i][0]);
+        const float al = M[i] == -INFINITY ? 0.0f : fast_exp2(M[i] - m_new);
+        const float be = ml[u][i][0] == -INFINITY ? 0.0f : fast_exp2(ml[u][i][0] - m_new);
+        M[i] = m_new;
+        L[i] = L[i] * al + ml[u][i][1] * be;
+        acc0[i] = acc0[i] * al + o0[u][i] * be;
+        acc1[i] = acc1[i] * al + o1[u][i] * be;
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < NH; ++i) {
+    if (!use[i]) continue;
+    const float inv = L[i] > 0.0f ? 1.0f / L[i] : 0.0f;
+    const f32x4 x0 = acc0[i] * inv, x1 = acc1[i] * inv;
+    u32x4 v;
+    if (a.f16) {
+      v[0] = pack_f16x2(x0[0], x0[1]);
+      v[1] = pack_f16x2(x0[2], x0[3]);
+      v[2] = pack_f16x2(x1[0], x1[1]);
+      v[3] = pack_f16x2(x1[2], x1[3]);
+    } else {
+      v[0] = pack_bf16x2(x0[0], x0[1]);
+      v[1] = pack_bf16x2(x0[2], x0[3]);
+      v[2] = pack_bf16x2(x1[0], x1[1]);
+      v[3] = pack_bf16x2(x1[2], x1[3]);
+    }
+    *reinterpret_cast<u32x4*>(a.out + (int64_t)q_row * a.out_ts + (int64_t)(h * a.g + cc[i]) * a.out_hs + 8 * j) = v;
+  }
+}
+
 // Log-sum-exp merge of the rows split across groups.  Wave k Hkv + h owns kv
 // head h of the row recorded by decode wave k Hkv + h (the row that crosses
 // the boundary after group k and starts inside group k's range); its
-// partials sit in wave
-// k Hkv + h (the recorded slot) and in waves x Hkv + h for groups x = k + 1
-// .. k_last (slot 0).  Lane l serves head 4 p + l / 16 of the group (pass p)
-// and head_dim elements 8 (l % 16) .. + 7; one pass over the partials keeps
-// a running max, sum and output, with the loads of four partials in flight
-// at a time.
+// partials sit in wave k Hkv + h (the recorded slot) and in waves x Hkv + h
+// for groups x = k + 1 .. k_last (slot 0).  Lane l serves head 4 p + l / 16
+// of the group (pass p) and head_dim elements 8 (l % 16) .. + 7; one pass
+// over the partials keeps a running max, sum and output, with the loads of
+// four partials in flight at a time, for up to two head passes together.
 __device__ __forceinline__ void merge_split_row(const DecodeArgs& a, int unit, int lane) {
   const int k = unit / a.Hkv, h = unit - k * a.Hkv;
   const int32_t* rec = a.ws_rec + 4 + 4 * unit;
@@ -62,52 +132,10 @@ __device__ __forceinline__ void merge_split_row(const DecodeArgs& a, int unit, i
   const int last = group_start(T, Kw, k + 1) - 1 + __builtin_amdgcn_readfirstlane(rec[1]);  // the row's last tile
   const int k_last = (int)(((int64_t)(last + 1) * Kw - 1) / T);
   const int slot_k = __builtin_amdgcn_readfirstlane(rec[2]);
-  const int j = lane & 15;
-  for (int c0 = 0; c0 < a.g; c0 += 4) {
-    const int c = c0 + (lane >> 4);
-    const bool use = c < a.g;
-    const int cc = use ? c : 0;
-    float M = -INFINITY, L = 0.0f;
-    f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-    for (int x0 = k; x0 <= k_last; x0 += 4) {
-      f32x2 ml[4];
-      f32x4 o0[4], o1[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int x = min(x0 + u, k_last);
-        const int64_t base = (((int64_t)x * a.Hkv + h) * 2 + (x == k ? slot_k : 0)) * a.g + cc;
-        ml[u] = *reinterpret_cast<const f32x2*>(a.ws_ml + base * 2);
-        o0[u] = *reinterpret_cast<const f32x4*>(a.ws_o + base * kHeadDim + 8 * j);
-        o1[u] = *reinterpret_cast<const f32x4*>(a.ws_o + base * kHeadDim + 8 * j + 4);
-      }
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        if (x0 + u > k_last) break;
-        const float m_new = fmaxf(M, ml[u][0]);
-        const float al = M == -INFINITY ? 0.0f : fast_exp2(M - m_new);
-        const float be = ml[u][0] == -INFINITY ? 0.0f : fast_exp2(ml[u][0] - m_new);
-        M = m_new;
-        L = L * al + ml[u][1] * be;
-        acc0 = acc0 * al + o0[u] * be;
-        acc1 = acc1 * al + o1[u] * be;
-      }
-    }
-    if (use) {
-      const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-      u32x4 v;
-      if (a.f16) {
-        v[0] = pack_f16x2(acc0[0] * inv, acc0[1] * inv);
-        v[1] = pack_f16x2(acc0[2] * inv, acc0[3] * inv);
-        v[2] = pack_f16x2(acc1[0] * inv, acc1[1] * inv);
-        v[3] = pack_f16x2(acc1[2] * inv, acc1[3] * inv);
-      } else {
-        v[0] = pack_bf16x2(acc0[0] * inv, acc0[1] * inv);
-        v[1] = pack_bf16x2(acc0[2] * inv, acc0[3] * inv);
-        v[2] = pack_bf16x2(acc1[0] * inv, acc1[1] * inv);
-        v[3] = pack_bf16x2(acc1[2] * inv, acc1[3] * inv);
-      }
-      *reinterpret_cast<u32x4*>(a.out + (int64_t)q_row * a.out_ts + (int64_t)(h * a.g + c) * a.out_hs + 8 * j) = v;
-    }
+  if (a.g <= 4) {
+    merge_heads<1>(a, h, k, k_last, slot_k, q_row, 0, lane);
+  } else {
+    for (int c0 = 0; c0 < a.g; c0 += 8) merge_heads<2>(a, h, k, k_last, slot_k, q_row, c0, lane);
   }
 }
 
