@@ -1,6 +1,8 @@
 // C ABI of the attention kernels: argument validation and dispatch of decode
 // rows (q_len == 1, split-K decode) and prefill rows (MFMA flash prefill).
 #include <algorithm>
+#include <cstdlib>
+#include <string>
 
 #include "nvs_common.h"
 #include "attention_common.h"
@@ -110,6 +112,41 @@ static bool shadow_serves(const AttnParams& P) {
   return prefill_mx_serves(C);
 }
 
+// Work-groups of a prefill launch that also streams the call's decode rows
+// (0: the decode keeps a launch of its own).  Every work-group slot of the
+// device, when the tile-loop kernel serves the prefill rows from a bf16 or
+// fp16 cache, the step's new tokens are already stored, and the device
+// holds two decode waves per kv head on each XCD.  Code caches keep the
+// decode launch: their decode waves, alone on a SIMD, streamed 17 GB/s a CU
+// (the bf16 ones 28) and the call ran slower than with the decode first.
+// NVS_CODECODE=0 turns it off.
+static int co_decode_wgs(const AttnParams& P) {
+  static const bool off = [] {
+    const char* e = std::getenv("NVS_CODECODE");
+    return e && std::string(e) == "0";
+  }();
+  if (off || P.kn || P.max_seqlen_q <= 1) return 0;
+  if (P.cache_dtype != NVS_DTYPE_BF16 && P.cache_dtype != NVS_DTYPE_FP16) return 0;
+  const int wgs = device_slots(1) & ~7;
+  return wgs >= std::max(8, (2 * P.Hkv + 7) & ~7) ? wgs : 0;
+}
+
+static float env_rate(const char* name, float dflt) {
+  const char* e = std::getenv(name);
+  return e ? std::strtof(e, nullptr) : dflt;
+}
+
+// Decode beside the prefill: a work-group of four decode waves (one per
+// SIMD) streams about 28 GB/s of bf16 decode rows while the other CUs run
+// prefill tiles (mixed_32b's 3.56 GB on 56 CUs in 2.3 ms), the chip about
+// 6 TB/s; a CU runs about 5 TFLOP/s of prefill (1.89 TFLOP in 1.47 ms on
+// 256 CUs).
+CoDecodeRates co_decode_rates() {
+  static const CoDecodeRates r = {env_rate("NVS_CODECODE_CU_BPS", 28e9f), env_rate("NVS_CODECODE_HBM_BPS", 6.0e12f),
+                                  env_rate("NVS_CODECODE_CU_FLOPS", 5.0e12f), env_rate("NVS_CODECODE_FINISH", 0.85f)};
+  return r;
+}
+
 int decode_launch_waves(int max_waves, int Hkv) {
   const int w = std::min(max_waves, device_slots(4 * kDecodeWavesPerEU));
   return std::max(Hkv, w / Hkv * Hkv);
@@ -201,6 +238,23 @@ static int paged_attention_impl(AttnParams& P, const void* q, int64_t q_tok_stri
                            : make_plan(workspace, P);
   char* partials = (char*)workspace + align256(plan_bytes(num_seqs, plan.ntq));
   const int max_waves = decode_wave_cap(num_seqs, max_seqlen_k, num_kv_heads);
+  // The tile-loop kernel serving the prefill rows streams the decode rows
+  // too (its first work-groups, before they join the prefill); the merge of
+  // split rows follows it.
+  const int co_wgs = (!shadow && prefill_mx_serves(P)) ? co_decode_wgs(P) : 0;
+  if (co_wgs > 0) {
+    CoDecode co;
+    co.a = decode_args(P, max_waves, partials);
+    co.bt = P.bt;
+    co.kv = P.cache_dtype;
+    co.groups = std::min(8 * ((co_wgs / 2) / P.Hkv), max_waves / P.Hkv);
+    co.wgs = co_wgs;
+    rc = launch_plan(P, plan, /*paged=*/true, s, nullptr, nullptr, &co);
+    if (rc != NVS_OK) return rc;
+    rc = launch_prefill_mx(P, plan, s, &co);
+    if (rc != NVS_OK) return rc;
+    return launch_decode_merge(co.a, co.groups, s);
+  }
   // With prefill rows the plan launch also merges the split decode rows.
   MergeJob merge;
   rc = launch_decode(P, max_waves, decode_launch_waves(max_waves, num_kv_heads), partials, s,

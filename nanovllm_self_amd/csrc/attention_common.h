@@ -98,7 +98,8 @@ struct PlanHeader {
   int prefill_next[8];  // per-XCD work counters of the prefill kernel (zeroed by the plan)
   int shadow_tiles;     // code caches: 64-key tiles of the prefill rows' bf16 copy
   int shadow_on;        // 1: the copy fits and the tile-loop kernel serves the prefill
-  int pad[53];          // keeps the list 256-byte aligned
+  int dec_wgs;          // work-groups of the prefill launch that stream the decode rows first
+  int pad[52];          // keeps the list 256-byte aligned
 };
 static_assert(sizeof(PlanHeader) == 256, "plan header is one 256-byte line");
 
@@ -257,10 +258,22 @@ int64_t attention_workspace_bytes(int num_seqs, int max_seqlen_q, int max_seqlen
 // smaller.
 int decode_launch_waves(int max_waves, int Hkv);
 struct MergeJob;
+struct CoDecode;
 // The plan kernel; with `merge` it also runs the decode launch's merge of
-// split rows (extra work-groups beside the plan's).
+// split rows (extra work-groups beside the plan's); with `co` it sizes the
+// decode part of the prefill launch (PlanHeader::dec_wgs) and clears the
+// decode waves' header.
 int launch_plan(const AttnParams& P, const Plan& plan, bool paged, hipStream_t stream,
-                const ShadowLayout* shadow = nullptr, const MergeJob* merge = nullptr);
+                const ShadowLayout* shadow = nullptr, const MergeJob* merge = nullptr,
+                const CoDecode* co = nullptr);
+// Rates the plan sizes the co-scheduled decode with: decode bytes per
+// second of one CU beside the prefill and of the whole chip, prefill FLOP
+// per second of one CU, and the fraction of the call by which the decode
+// should end.
+struct CoDecodeRates {
+  float cu_bps, hbm_bps, pre_cu_flops, finish;
+};
+CoDecodeRates co_decode_rates();
 // Dequantises the prefill rows' tiles into the copy (runs only where the
 // plan set shadow_on).
 int launch_shadow_fill(const AttnParams& P, const Plan& plan, const ShadowLayout& sh, hipStream_t stream);
@@ -268,12 +281,21 @@ int launch_shadow_fill(const AttnParams& P, const Plan& plan, const ShadowLayout
 // `defer`, left to the plan launch (defer receives what it needs).
 int launch_decode(const AttnParams& P, int max_waves, int waves, void* partials, hipStream_t stream,
                   MergeJob* defer = nullptr);
+// The decode waves' arguments (partials for max_waves waves at `partials`),
+// and the merge of rows split across `groups` decode groups as a launch.
+struct DecodeArgs;
+DecodeArgs decode_args(const AttnParams& P, int max_waves, void* partials);
+int launch_decode_merge(const DecodeArgs& a, int groups, hipStream_t stream);
 int launch_prefill(const AttnParams& P, const Plan& plan, hipStream_t stream);
 // The MFMA tile-loop prefill kernel (paged_prefill_mx.hip): whether it serves
 // a call, its query positions per work item for a group of g query heads,
 // and its launch.
 bool prefill_mx_serves(const AttnParams& P);
 int prefill_mx_positions(int g);
-int launch_prefill_mx(const AttnParams& P, const Plan& plan, hipStream_t stream);
+// With `co`, the launch's first work-groups stream the call's decode rows
+// before they join the prefill (co->kv: the cache type of the decode rows,
+// which a code cache's prefill reads through its bf16 copy); the plan has
+// sized their number for co->wgs work-groups.
+int launch_prefill_mx(const AttnParams& P, const Plan& plan, hipStream_t stream, const CoDecode* co = nullptr);
 
 }  // namespace nvs

@@ -1,7 +1,8 @@
-// The decode kernel's arguments and the merge of its split rows, shared by
-// the decode file (the merge's own launch, for decode-only calls) and the
-// planning kernel (which runs the merge beside the plan in one launch when a
-// paged call also has prefill rows).
+// The decode waves' arguments and the merge of their split rows, shared by
+// the decode file (the merge's own launch: decode-only calls, and calls
+// whose prefill launch streamed the decode rows) and the planning kernel
+// (which runs the merge beside the plan in one launch when a paged call's
+// decode launch comes before prefill rows).
 #pragma once
 
 #include "nvs_common.h"
@@ -124,10 +125,13 @@ __device__ __forceinline__ void merge_heads(const DecodeArgs& a, int h, int k, i
 // four partials in flight at a time, for up to two head passes together.
 __device__ __forceinline__ void merge_split_row(const DecodeArgs& a, int unit, int lane) {
   const int k = unit / a.Hkv, h = unit - k * a.Hkv;
+  // Groups k >= Kw - 1 merge nothing (a launch may hold more merge waves
+  // than the decode had groups; their records are not this call's).
+  const int Kw = __builtin_amdgcn_readfirstlane(a.ws_rec[1]);
+  if (k >= Kw - 1) return;
   const int32_t* rec = a.ws_rec + 4 + 4 * unit;
   if (__builtin_amdgcn_readfirstlane(rec[3]) == 0) return;
   const int T = __builtin_amdgcn_readfirstlane(a.ws_rec[0]);
-  const int Kw = __builtin_amdgcn_readfirstlane(a.ws_rec[1]);
   const int q_row = __builtin_amdgcn_readfirstlane(rec[0]);
   const int last = group_start(T, Kw, k + 1) - 1 + __builtin_amdgcn_readfirstlane(rec[1]);  // the row's last tile
   const int k_last = (int)(((int64_t)(last + 1) * Kw - 1) / T);
@@ -144,6 +148,17 @@ __device__ __forceinline__ void merge_split_row(const DecodeArgs& a, int unit, i
 struct MergeJob {
   DecodeArgs a;
   int units;
+};
+
+// Decode rows streamed by the MFMA prefill launch: their arguments and
+// block tables, the cache type, the decode groups the partial workspace
+// holds, and the work-groups the launch runs.
+struct CoDecode {
+  DecodeArgs a;
+  const int32_t* bt;
+  int kv;
+  int groups;
+  int wgs;
 };
 
 }  // namespace nvs

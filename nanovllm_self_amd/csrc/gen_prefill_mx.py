@@ -56,9 +56,9 @@ Register map (fixed; the C++ side binds inputs to it):
   v232-239 exponential temporaries, v240 block id, v241-242 row sums,
   v243 claim, v244-245 the previous unit's l, v246 output lane offset,
   v247 (lane % 32) - 4 (lane / 32), v248 constants (BANKC_* lanes),
-  v249-251 unit banks (next, current, previous), v252 plan record,
-  v253 4 x lane, v254 bank of the unit after next, v255 output staging
-  read address
+  v249-251 unit banks (next, current, previous), v252 plan record and,
+  decoded over it, the bank of the unit after next, v253-254 unused (left to the compiler for the spill lanes of the code
+  before the statement), v255 output staging read address
   a[0:63]     Q^T operands: Q[qb][st] = a[32 qb + 4 st ..]
   a[64:191]   O^T accumulators: O[n][qb] = a[64 + 16 (2 n + qb) ..]
   a[192:223]  V operand ring (8 slots), a[224:255] K operand ring (8 slots)
@@ -145,8 +145,7 @@ LANEC = "v247"       # (lane % 32) - 4 (lane / 32): the mask limit's lane part
 BANKC = "v248"       # call constants, lane BANKC_*
 BANKN, BANKU, BANKP = "v249", "v250", "v251"  # unit descriptors, lane BANK_*
 VREC = "v252"        # plan record of the unit after next, dword k in lane k
-V4L = "v253"         # 4 x lane
-BANKN2 = "v254"      # the unit after next, decoded
+BANKN2 = VREC        # the unit after next, decoded over its plan record (read first)
 RL = "v255"          # query stage read address of output row lane / 16, chunk lane % 16
 
 # BANKC lanes: call (and wave) constants
@@ -646,7 +645,11 @@ def record_load_items(u):
         f"s_and_b32 {S_RREC_W[1]}, {S_RREC_W[1]}, 0xffff",
         f"s_mov_b32 {S_RREC_W[2]}, 64",
         f"s_mov_b32 {S_RREC_W[3]}, {RSRC_W3}",
-        f"buffer_load_dword {VREC}, {V4L}, {S_RREC}, 0 offen",
+        # lane offsets 4 x lane, in VREC itself (its last record is decoded)
+        f"v_mbcnt_lo_u32_b32 {VREC}, -1, 0",
+        f"v_mbcnt_hi_u32_b32 {VREC}, -1, {VREC}",
+        f"v_lshlrev_b32 {VREC}, 2, {VREC}",
+        f"buffer_load_dword {VREC}, {VREC}, {S_RREC}, 0 offen",
     ]
     return it
 
@@ -1106,12 +1109,13 @@ def block_iteration(em, paged, par, kind, lbl):
         for i in range(AHEAD):
             k_read(em, spar, i)
     else:
-        lead = 8  # VALU work before the first MFMA waits for its operand
+        lead = 0  # VALU work before the first MFMA (none: measured fastest of 0, 2, 4, 6, 8, 12)
         emit_items(em, a_items[:lead])
-        # the fill's scalar setup and loads share the first 16 slots
+        # the fill's scalar setup and loads share the first 24 slots (of 8,
+        # 16, 24 or 32: measured fastest)
         slots = spread(a_items[lead:], 32)
-        fs = spread(fill, 16)
-        for k in range(16):
+        fs = spread(fill, 24)
+        for k in range(24):
             slots[k] = fs[k] + slots[k]
         for i in range(16):
             em.lds_wait(("v", i, 1))
@@ -1427,7 +1431,7 @@ def program(paged):
 INPUT_REGS = set()  # filled from the C++ operand list by the checker
 CLOBBERS = (
     [f"v{i}" for i in range(0, 192)] + [f"v{i}" for i in range(216, 246)] + [f"v{i}" for i in range(249, 253)]
-    + ["v254"] + [f"a{i}" for i in range(0, 256)]
+    + [f"a{i}" for i in range(0, 256)]
     + [f"s{i}" for i in range(24, 32)] + [f"s{i}" for i in range(34, 37)] + ["s38", "s39"]
     + [f"s{i}" for i in range(40, 54)] + [f"s{i}" for i in range(56, 60)] + [f"s{i}" for i in range(64, 100)]
     + ["vcc", "scc", "m0", "memory"]

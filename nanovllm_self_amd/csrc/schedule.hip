@@ -21,6 +21,19 @@ struct PlanArgs {
   int shadow_cap;
   int shadow_st;     // tiles of a table row: a row's tiles past it are not copied
   int64_t Tk;        // rows of the local k / v (local mode)
+  // Decode rows streamed by the prefill launch's first work-groups (co_wgs
+  // > 0: the launch's work-group count; 0: the decode has a launch of its
+  // own).  The plan picks how many from the decode bytes and the prefill
+  // FLOPs at the per-CU rates below.
+  int co_wgs;
+  int32_t* dec_rec;  // the decode waves' header (T, Kw), zeroed here: with no decode work-group the
+                     // merge after the prefill launch must find no groups, not a stale count
+  int Hq, Hkv;
+  float dec_tile_bytes;  // HBM bytes of one 32-key decode tile over all kv heads
+  float dec_cu_bps;      // decode bytes per second one CU streams beside the prefill
+  float dec_hbm_bps;     // decode bytes per second of the whole chip
+  float pre_cu_flops;    // prefill FLOP per second of one CU
+  float dec_finish;      // the decode should end by this fraction of the call
 };
 
 // Tiles of the bf16 copy for a prefill row with kl keys.
@@ -82,6 +95,49 @@ __device__ __forceinline__ void row_work(const PlanArgs& a, int b, bool& dec, in
 constexpr int kPlanThreads = 1024;
 constexpr int kPlanWaves = kPlanThreads / 64;
 
+// Sum of one float per thread over the 1024-thread work-group (every thread
+// gets it).  Two barriers.
+__device__ __forceinline__ float block_sum_1024(float v, float* lds) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  if (lane == 0) lds[w] = v;
+  __syncthreads();
+  float all = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kPlanWaves; ++i) all += lds[i];
+  __syncthreads();
+  return all;
+}
+
+// Query-key pairs of a prefill row with L new and K visible keys under the
+// causal mask (row r sees keys j <= r + K - L).
+__device__ __forceinline__ float causal_pairs(int L, int K) {
+  const float off = (float)(K - L);
+  return K >= L ? (float)L * off + 0.5f * (float)L * (float)(L + 1) : 0.5f * (float)K * (float)(K + 1);
+}
+
+// Work-groups of the prefill launch that stream the decode rows before they
+// join the prefill: the fewest (a multiple of 8, one per XCD at a time, and
+// at least two waves per kv head) whose decode, at dec_cu_bps a CU and at
+// most dec_hbm_bps in all, ends by dec_finish of the call's estimated time,
+// the prefill's CU time (FLOPs at pre_cu_flops a CU) plus the decode's
+// shared by all work-groups; all of them when none does; none without
+// decode rows.
+__device__ int pick_decode_wgs(const PlanArgs& a, float dec_rows, float dec_tiles, float pairs) {
+  if (a.co_wgs <= 0 || dec_rows <= 0.0f) return 0;  // a keyless decode row still needs its zeros
+  const int top = a.co_wgs & ~7;
+  const int lo = min(top, max(8, (2 * a.Hkv + 7) & ~7));
+  const float bytes = dec_tiles * a.dec_tile_bytes;
+  const float pre = pairs * 4.0f * (float)a.Hq * (float)kHeadDim / a.pre_cu_flops;  // CU seconds
+  for (int nd = lo; nd <= top; nd += 8) {
+    const float td = bytes / fminf((float)nd * a.dec_cu_bps, a.dec_hbm_bps);
+    const float t = (pre + (float)nd * td) / (float)a.co_wgs;
+    if (td <= a.dec_finish * t) return nd;
+  }
+  return top;
+}
+
 // What the plan keeps of each row of a 1024-row step in LDS while the
 // step's list entries are written, one entry per thread.
 struct PlanRows {
@@ -100,6 +156,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanArgs a, DecodeAr
     return;
   }
   __shared__ int scan_lds[kPlanWaves];
+  __shared__ float sum_lds[kPlanWaves];
   __shared__ PlanRows rows;
   const int tid = threadIdx.x;
   const Plan& pl = a.plan;
@@ -136,11 +193,16 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanArgs a, DecodeAr
   // once and from L2 after that.  Each thread then writes entries e, e +
   // 1024, ... of the step, finding its row by a binary search of the prefix.
   int base = 0;
+  // this thread's rows: decode rows and their tiles, prefill query-key pairs
+  float dec_rows = 0.0f, dec_tiles = 0.0f, pairs = 0.0f;
   for (int b0 = 0; b0 < a.B; b0 += kPlanThreads) {
     bool dec;
     int np, q0, kl, tot;
     const int b = b0 + tid;
     row_work(a, b, dec, np, q0, kl);
+    if (dec) dec_rows += 1.0f;
+    if (dec && kl > 0) dec_tiles += (float)((kl + kDecodeTile - 1) / kDecodeTile);
+    if (np > 0) pairs += causal_pairs(a.cu_q[b + 1] - q0, kl);
     const int incl = block_scan_1024(np, scan_lds, tot);
     rows.end[tid] = incl;
     if (np > 0) {
@@ -201,6 +263,15 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanArgs a, DecodeAr
     base += tot;
   }
   if (tid == 0) pl.hdr->n_prefill = base;
+  if (a.co_wgs > 0) {
+    if (tid < 2) a.dec_rec[tid] = 0;
+    dec_rows = block_sum_1024(dec_rows, sum_lds);
+    dec_tiles = block_sum_1024(dec_tiles, sum_lds);
+    pairs = block_sum_1024(pairs, sum_lds);
+    if (tid == 0) pl.hdr->dec_wgs = pick_decode_wgs(a, dec_rows, dec_tiles, pairs);
+  } else if (tid == 0) {
+    pl.hdr->dec_wgs = 0;
+  }
 }
 
 static int g_cus[64] = {0};
@@ -218,7 +289,7 @@ int device_slots(int per_cu) {
 }
 
 int launch_plan(const AttnParams& P, const Plan& plan, bool paged, hipStream_t stream, const ShadowLayout* shadow,
-                const MergeJob* merge) {
+                const MergeJob* merge, const CoDecode* co) {
   PlanArgs a;
   a.cu_q = P.cu_q;
   a.cu_k = P.cu_k;
@@ -234,6 +305,17 @@ int launch_plan(const AttnParams& P, const Plan& plan, bool paged, hipStream_t s
   a.shadow_cap = shadow ? shadow->cap : 0;
   a.shadow_st = shadow ? shadow->ST : 0;
   a.Tk = P.Tk;
+  a.co_wgs = co ? co->wgs : 0;
+  a.dec_rec = co ? co->a.ws_rec : nullptr;
+  a.Hq = P.Hq;
+  a.Hkv = P.Hkv;
+  const float esz = (P.cache_dtype == NVS_DTYPE_BF16 || P.cache_dtype == NVS_DTYPE_FP16) ? 2.0f : 1.0f;
+  a.dec_tile_bytes = (float)kDecodeTile * P.Hkv * (2.0f * kHeadDim * esz + (esz < 2.0f ? 8.0f : 0.0f));
+  const CoDecodeRates r = co_decode_rates();
+  a.dec_cu_bps = r.cu_bps;
+  a.dec_hbm_bps = r.hbm_bps;
+  a.pre_cu_flops = r.pre_cu_flops;
+  a.dec_finish = r.finish;
   DecodeArgs m = {};
   int units = 0;
   if (merge && merge->units > 0) {
