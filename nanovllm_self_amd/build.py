@@ -32,6 +32,10 @@ COMMON_FLAGS = [
     "-Wno-unused-function",
     "-Wno-unused-variable",
 ]
+# The MFMA prefill kernel runs compiled decode code beside its asm statement
+# at one wave per SIMD, where the compiler would otherwise keep the decode
+# accumulators in AGPRs and copy them to and from VGPRs every tile.
+FILE_FLAGS = {"paged_prefill_mx.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def hipcc() -> str:
@@ -43,7 +47,7 @@ def hipcc() -> str:
 
 def _compile(src: Path) -> Path:
     obj = BUILD_DIR / (src.stem + ".o")
-    cmd = [hipcc(), *COMMON_FLAGS, *DEVICE_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *COMMON_FLAGS, *DEVICE_FLAGS, *FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     # The host pass does not know the device-only feature; drop that warning.
     noise = "-packed-fp32-ops' is not a recognized feature"

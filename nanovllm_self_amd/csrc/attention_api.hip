@@ -113,12 +113,10 @@ static bool shadow_serves(const AttnParams& P) {
 }
 
 // Work-groups of a prefill launch that also streams the call's decode rows
-// (0: the decode keeps a launch of its own).  Every work-group slot of the
-// device, when the tile-loop kernel serves the prefill rows from a bf16 or
-// fp16 cache, the step's new tokens are already stored, and the device
-// holds two decode waves per kv head on each XCD.  Code caches keep the
-// decode launch: their decode waves, alone on a SIMD, streamed 17 GB/s a CU
-// (the bf16 ones 28) and the call ran slower than with the decode first.
+// (0: the decode keeps a launch of its own): every work-group slot of the
+// device, when the tile-loop kernel serves the prefill rows (from the cache,
+// or from a code cache's bf16 copy), the step's new tokens are already
+// stored, and the device holds two decode waves per kv head on each XCD.
 // NVS_CODECODE=0 turns it off.
 static int co_decode_wgs(const AttnParams& P) {
   static const bool off = [] {
@@ -126,7 +124,6 @@ static int co_decode_wgs(const AttnParams& P) {
     return e && std::string(e) == "0";
   }();
   if (off || P.kn || P.max_seqlen_q <= 1) return 0;
-  if (P.cache_dtype != NVS_DTYPE_BF16 && P.cache_dtype != NVS_DTYPE_FP16) return 0;
   const int wgs = device_slots(1) & ~7;
   return wgs >= std::max(8, (2 * P.Hkv + 7) & ~7) ? wgs : 0;
 }
@@ -137,14 +134,20 @@ static float env_rate(const char* name, float dflt) {
 }
 
 // Decode beside the prefill: a work-group of four decode waves (one per
-// SIMD) streams about 28 GB/s of bf16 decode rows while the other CUs run
-// prefill tiles (mixed_32b's 3.56 GB on 56 CUs in 2.3 ms), the chip about
-// 6 TB/s; a CU runs about 5 TFLOP/s of prefill (1.89 TFLOP in 1.47 ms on
-// 256 CUs).
-CoDecodeRates co_decode_rates() {
-  static const CoDecodeRates r = {env_rate("NVS_CODECODE_CU_BPS", 28e9f), env_rate("NVS_CODECODE_HBM_BPS", 6.0e12f),
+// SIMD) streams about 44 GB/s of a bf16 cache's decode rows while the other
+// CUs run prefill tiles (mixed_32b's 3.56 GB on 32 CUs in 2.5 ms) and about
+// 28 GB/s of an fp8 one's (1.84 GB on 32 CUs in 2.3 ms: a code tile carries
+// half the bytes for the same VALU work), the chip about 6 TB/s; a CU runs
+// about 5 TFLOP/s of prefill (1.89 TFLOP in 1.47 ms on 256 CUs).
+// NVS_CODECODE_{CU_BPS,HBM_BPS,CU_FLOPS,FINISH} override them.
+CoDecodeRates co_decode_rates(int cache_dtype) {
+  const bool half = cache_dtype == NVS_DTYPE_BF16 || cache_dtype == NVS_DTYPE_FP16;
+  static const float cu16 = env_rate("NVS_CODECODE_CU_BPS", 44e9f), cu8 = env_rate("NVS_CODECODE_CU_BPS", 28e9f);
+  static const CoDecodeRates r = {0.0f, env_rate("NVS_CODECODE_HBM_BPS", 6.0e12f),
                                   env_rate("NVS_CODECODE_CU_FLOPS", 5.0e12f), env_rate("NVS_CODECODE_FINISH", 0.85f)};
-  return r;
+  CoDecodeRates x = r;
+  x.cu_bps = half ? cu16 : cu8;
+  return x;
 }
 
 int decode_launch_waves(int max_waves, int Hkv) {
@@ -241,7 +244,7 @@ static int paged_attention_impl(AttnParams& P, const void* q, int64_t q_tok_stri
   // The tile-loop kernel serving the prefill rows streams the decode rows
   // too (its first work-groups, before they join the prefill); the merge of
   // split rows follows it.
-  const int co_wgs = (!shadow && prefill_mx_serves(P)) ? co_decode_wgs(P) : 0;
+  const int co_wgs = (shadow || prefill_mx_serves(P)) ? co_decode_wgs(P) : 0;
   if (co_wgs > 0) {
     CoDecode co;
     co.a = decode_args(P, max_waves, partials);
@@ -249,10 +252,34 @@ static int paged_attention_impl(AttnParams& P, const void* q, int64_t q_tok_stri
     co.kv = P.cache_dtype;
     co.groups = std::min(8 * ((co_wgs / 2) / P.Hkv), max_waves / P.Hkv);
     co.wgs = co_wgs;
-    rc = launch_plan(P, plan, /*paged=*/true, s, nullptr, nullptr, &co);
+    if (!shadow) {
+      rc = launch_plan(P, plan, /*paged=*/true, s, nullptr, nullptr, &co);
+      if (rc != NVS_OK) return rc;
+      rc = launch_prefill_mx(P, plan, s, &co);
+      if (rc != NVS_OK) return rc;
+      return launch_decode_merge(co.a, co.groups, s);
+    }
+    // Code cache: the prefill reads the bf16 copy, the decode waves the
+    // codes; they run whichever prefill kernel the plan lets serve.
+    const ShadowLayout sh = shadow_at((char*)workspace + align256(attention_workspace_bytes(
+                                          P.B, P.max_seqlen_q, P.max_seqlen_k, P.Hq, P.Hkv)),
+                                      P.B, P.max_seqlen_k, P.Hkv);
+    rc = launch_plan(P, plan, /*paged=*/true, s, &sh, nullptr, &co);
     if (rc != NVS_OK) return rc;
-    rc = launch_prefill_mx(P, plan, s, &co);
+    rc = launch_shadow_fill(P, plan, sh, s);
     if (rc != NVS_OK) return rc;
+    AttnParams C = P;
+    C.kc = sh.k; C.vc = sh.v; C.cache_dtype = NVS_DTYPE_BF16; C.ks = nullptr; C.vs = nullptr;
+    C.bt = sh.table; C.bt_stride = sh.ST; C.bs = kShadowTile; C.NB = sh.cap;
+    C.gate = &plan.hdr->shadow_on; C.gate_run = 1;
+    rc = launch_prefill_mx(C, plan, s, &co);
+    if (rc != NVS_OK) return rc;
+    if ((int64_t)sh.cap < (int64_t)P.B * sh.ST) {
+      AttnParams F = P;
+      F.gate = &plan.hdr->shadow_on; F.gate_run = 0;
+      rc = launch_prefill(F, plan, s);
+      if (rc != NVS_OK) return rc;
+    }
     return launch_decode_merge(co.a, co.groups, s);
   }
   // With prefill rows the plan launch also merges the split decode rows.

@@ -273,7 +273,7 @@ int launch_plan(const AttnParams& P, const Plan& plan, bool paged, hipStream_t s
 struct CoDecodeRates {
   float cu_bps, hbm_bps, pre_cu_flops, finish;
 };
-CoDecodeRates co_decode_rates();
+CoDecodeRates co_decode_rates(int cache_dtype);
 // Dequantises the prefill rows' tiles into the copy (runs only where the
 // plan set shadow_on).
 int launch_shadow_fill(const AttnParams& P, const Plan& plan, const ShadowLayout& sh, hipStream_t stream);

@@ -15,6 +15,16 @@
 
 namespace nvs {
 
+// Element i of a read-only input (block tables, cu_seqlens) at a
+// wave-uniform index, as a scalar load: through the constant address space
+// the compiler issues s_load whatever the kernel stores elsewhere.  As a
+// vector load, its wait (followed by readfirstlane) would also wait for
+// every tile load the wave has in flight.
+template <typename T>
+__device__ __forceinline__ T scalar_read(const T* p, int64_t i) {
+  return ((const __attribute__((address_space(4))) T*)p)[i];
+}
+
 // Caches of 16-bit values (bf16, fp16) share the tile layout and loads; the
 // MFMA and the packing of P and of the output follow the element type.
 // Code caches compute in bf16.
@@ -100,14 +110,15 @@ __device__ __forceinline__ LaneOffsets lane_offsets(int Hkv, int col, int grp) {
 // (16 key rows x 64 bytes), the other half coming with the next instruction:
 // K stays a plain load, since an `nt` line can leave the cache in between
 // (K marked `nt` as well: fp8 233 -> 240 us, bf16 428 -> 429 us).
-#ifndef NVS_DECODE_NT
-#define NVS_DECODE_NT 1
-#endif
-template <typename T>
-__device__ __forceinline__ T v_load(const T* p) {
-  if constexpr (NVS_DECODE_NT) return __builtin_nontemporal_load(p);
-  else return *p;
-}
+//
+// V is read through a buffer resource whose base is the tile's first row:
+// the loop-invariant lane offset and the slot's row offset (a scalar) form
+// each address.  Built as 64-bit lane addresses instead, the compiler reused
+// one address register as the destination of a V load, and since the loop
+// can reach its next iteration from either unrolled step, it then waited
+// for every load in flight (vmcnt(0)) at each step before issuing the next
+// tile's loads: a wave had one tile in flight, not D - 1.
+constexpr int kNtAux = 2;  // the `nt` bit of a buffer load's cache policy
 
 // Loads of one 32-key tile of kv head h whose first key sits at offset koff
 // of pool block blk (-1: missing; the loads then read block 0, in bounds).
@@ -121,14 +132,19 @@ __device__ __forceinline__ void decode_load(DecodeTile<KV>& T, const DecodeArgs&
   const int64_t rowb = (int64_t)a.Hkv * kHeadDim * ESZ;  // bytes per token row
   const char* kb = (const char*)a.kc + row0 * kHeadDim * ESZ;
   const char* vb = (const char*)a.vc + row0 * kHeadDim * ESZ;
-  const uint32_t ok = lane_off(lo.k), ov = lane_off(lo.v);
+  const uint32_t ok = lane_off(lo.k);
+  // num_records past any row offset a tile uses; a raw buffer's loads are
+  // range-checked against it (an access past it reads 0).
+  const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc((void*)vb, 0, 0x7fffffff, 0x20000);
   if constexpr (kHalf<KV>) {
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int s = 0; s < 4; ++s) T.k[t][s] = *reinterpret_cast<const u32x4*>(kb + 16 * t * rowb + 64 * s + ok);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) T.v[e] = v_load(reinterpret_cast<const u32x4*>(vb + slot_key(e, 0) * rowb + ov));
+    for (int e = 0; e < 8; ++e)
+      T.v[e] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vr, lo.v, (int)(slot_key(e, 0) * rowb),
+                                                                                kNtAux));
   } else {
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
@@ -136,7 +152,9 @@ __device__ __forceinline__ void decode_load(DecodeTile<KV>& T, const DecodeArgs&
       T.k[t][1] = *reinterpret_cast<const u32x4*>(kb + 16 * t * rowb + 16 + ok);
     }
 #pragma unroll
-    for (int e = 0; e < 8; ++e) T.v[e] = v_load(reinterpret_cast<const u32x2*>(vb + slot_key(e, 0) * rowb + ov));
+    for (int e = 0; e < 8; ++e)
+      T.v[e] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(vr, lo.v, (int)(slot_key(e, 0) * rowb),
+                                                                               kNtAux));
     // One scale per lane (lanes 0-31 the k scales of the tile's keys, 32-63
     // the v scales); the compute hands each lane its keys' scales with
     // cross-lane reads.
@@ -356,9 +374,9 @@ struct RowInfo {
 __device__ __forceinline__ RowInfo row_info(const DecodeArgs& a, const int32_t* __restrict__ cu_q,
                                             const int32_t* __restrict__ cu_k, int b) {
   RowInfo r;
-  r.q0 = cu_q[b];
-  const int q1 = cu_q[b + 1];
-  r.K = cu_k[b + 1] - cu_k[b];
+  r.q0 = scalar_read(cu_q, b);
+  const int q1 = scalar_read(cu_q, b + 1);
+  r.K = scalar_read(cu_k, b + 1) - scalar_read(cu_k, b);
   r.dec = q1 - r.q0 == 1 && r.q0 >= 0 && (int64_t)q1 <= a.T;
   return r;
 }
@@ -674,13 +692,18 @@ __device__ __forceinline__ void next_row(const DecodeArgs& a, const int32_t* __r
 // Block id of cursor c's tile (-1 where the table has none or it is outside
 // the pool); a 32-key tile never spans two blocks (block_size % 64 == 0).
 __device__ __forceinline__ int tile_block(const DecodeArgs& a, const int32_t* __restrict__ bt, const Cursor& c) {
-  const int blk = c.lb < a.bt_stride ? bt[(int64_t)c.b * a.bt_stride + c.lb] : -1;
+  const int blk = c.lb < a.bt_stride ? scalar_read(bt, (int64_t)c.b * a.bt_stride + c.lb) : -1;
   return (blk >= 0 && blk < a.NB) ? blk : -1;
 }
 
 // Q^T as the B operand for query row q0, kv head h: column = head (col < g);
 // step s, lane group grp holds the same 8 d values as the K operand: d = 32 s
-// + 8 grp for bf16 caches, 32 grp + 8 s for code caches.
+// + 8 grp for bf16 caches, 32 grp + 8 s for code caches.  Columns past the
+// group's heads hold head 0's values: every column's scores, softmax and
+// output are its own (the MFMAs never mix columns, the row max and sum
+// reduce over one column's lanes) and those columns are never stored.
+// Zeroing them would wait for the loads right away, and with them for every
+// tile load in flight; this way the wait falls at the next tile's MFMAs.
 template <int KV>
 __device__ __forceinline__ void load_q(bf16x8 (&qop)[4], const DecodeArgs& a, int q0, int h, int col, int grp) {
   const bool use = col < a.g;
@@ -690,10 +713,8 @@ __device__ __forceinline__ void load_q(bf16x8 (&qop)[4], const DecodeArgs& a, in
   const uint32_t lo =
       lane_off(((uint32_t)(use ? col : 0) * (uint32_t)a.q_hs + kKGroupStride<KV> * grp) * 2u);
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    const u32x4 x = *reinterpret_cast<const u32x4*>(qb + lo + kKStepStride<KV> * s * 2);
-    qop[s] = __builtin_bit_cast(bf16x8, use ? x : u32x4{0, 0, 0, 0});
-  }
+  for (int s = 0; s < 4; ++s)
+    qop[s] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(qb + lo + kKStepStride<KV> * s * 2));
 }
 
 // The end of a row segment of kv head h: a row the wave saw whole is
@@ -805,7 +826,7 @@ __device__ __forceinline__ void decode_wave(const DecodeArgs& a, const int32_t* 
       if (last >= s0 + left) break;  // the row ends in a later group's range
       const int64_t slot = a.slots[c.q0];
       const int lb = (c.K - 1) / a.bs;  // c.K >= 1: the row has tiles
-      const int blk = lb < a.bt_stride ? bt[(int64_t)c.b * a.bt_stride + lb] : -1;
+      const int blk = lb < a.bt_stride ? scalar_read(bt, (int64_t)c.b * a.bt_stride + lb) : -1;
       if (owner_writes(a, slot, blk, c.K - 1 - lb * a.bs)) {
         store_new_token<KV>(a, c.q0, slot, h);
         fence_tile = min(fence_tile, last);

@@ -118,19 +118,23 @@ __device__ __forceinline__ float causal_pairs(int L, int K) {
 }
 
 // Work-groups of the prefill launch that stream the decode rows before they
-// join the prefill: the fewest (a multiple of 8, one per XCD at a time, and
-// at least two waves per kv head) whose decode, at dec_cu_bps a CU and at
-// most dec_hbm_bps in all, ends by dec_finish of the call's estimated time,
-// the prefill's CU time (FLOPs at pre_cu_flops a CU) plus the decode's
-// shared by all work-groups; all of them when none does; none without
-// decode rows.
+// join the prefill: the fewest whose decode, at dec_cu_bps a CU and at most
+// dec_hbm_bps in all, ends by dec_finish of the call's estimated time (the
+// prefill's CU time, its FLOPs at pre_cu_flops a CU, plus the decode's,
+// shared by all work-groups); all of them when none does; none without
+// decode rows.  Counts step in multiples of 8 (as many on every XCD) and of
+// 2 Hkv (an XCD's decode waves form whole groups: at 24 work-groups and Hkv
+// = 8 a third of them idled) when the launch holds such a step.
 __device__ int pick_decode_wgs(const PlanArgs& a, float dec_rows, float dec_tiles, float pairs) {
   if (a.co_wgs <= 0 || dec_rows <= 0.0f) return 0;  // a keyless decode row still needs its zeros
   const int top = a.co_wgs & ~7;
-  const int lo = min(top, max(8, (2 * a.Hkv + 7) & ~7));
+  int step = 8;
+  while (step % (2 * a.Hkv) != 0 && step <= top) step += 8;
+  if (step > top) step = 8;
+  const int lo = min(top, max(step, (2 * a.Hkv + 7) & ~7));
   const float bytes = dec_tiles * a.dec_tile_bytes;
   const float pre = pairs * 4.0f * (float)a.Hq * (float)kHeadDim / a.pre_cu_flops;  // CU seconds
-  for (int nd = lo; nd <= top; nd += 8) {
+  for (int nd = lo; nd <= top; nd += step) {
     const float td = bytes / fminf((float)nd * a.dec_cu_bps, a.dec_hbm_bps);
     const float t = (pre + (float)nd * td) / (float)a.co_wgs;
     if (td <= a.dec_finish * t) return nd;
@@ -311,7 +315,7 @@ int launch_plan(const AttnParams& P, const Plan& plan, bool paged, hipStream_t s
   a.Hkv = P.Hkv;
   const float esz = (P.cache_dtype == NVS_DTYPE_BF16 || P.cache_dtype == NVS_DTYPE_FP16) ? 2.0f : 1.0f;
   a.dec_tile_bytes = (float)kDecodeTile * P.Hkv * (2.0f * kHeadDim * esz + (esz < 2.0f ? 8.0f : 0.0f));
-  const CoDecodeRates r = co_decode_rates();
+  const CoDecodeRates r = co_decode_rates(P.cache_dtype);
   a.dec_cu_bps = r.cu_bps;
   a.dec_hbm_bps = r.hbm_bps;
   a.pre_cu_flops = r.pre_cu_flops;
