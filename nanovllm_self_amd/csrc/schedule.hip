@@ -95,19 +95,25 @@ __device__ __forceinline__ void row_work(const PlanArgs& a, int b, bool& dec, in
 constexpr int kPlanThreads = 1024;
 constexpr int kPlanWaves = kPlanThreads / 64;
 
-// Sum of one float per thread over the 1024-thread work-group (every thread
-// gets it).  Two barriers.
-__device__ __forceinline__ float block_sum_1024(float v, float* lds) {
+// Sums of three floats per thread over the 1024-thread work-group (every
+// thread gets them).  Two barriers.
+__device__ __forceinline__ void block_sum3_1024(float (&v)[3], float (*lds)[3]) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-  if (lane == 0) lds[w] = v;
-  __syncthreads();
-  float all = 0.0f;
+  for (int i = 0; i < 3; ++i)
 #pragma unroll
-  for (int i = 0; i < kPlanWaves; ++i) all += lds[i];
+    for (int off = 32; off >= 1; off >>= 1) v[i] += __shfl_xor(v[i], off, 64);
+  if (lane == 0)
+    for (int i = 0; i < 3; ++i) lds[w][i] = v[i];
   __syncthreads();
-  return all;
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    float all = 0.0f;
+#pragma unroll
+    for (int x = 0; x < kPlanWaves; ++x) all += lds[x][i];
+    v[i] = all;
+  }
+  __syncthreads();
 }
 
 // Query-key pairs of a prefill row with L new and K visible keys under the
@@ -160,7 +166,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanArgs a, DecodeAr
     return;
   }
   __shared__ int scan_lds[kPlanWaves];
-  __shared__ float sum_lds[kPlanWaves];
+  __shared__ float sum_lds[kPlanWaves][3];
   __shared__ PlanRows rows;
   const int tid = threadIdx.x;
   const Plan& pl = a.plan;
@@ -269,10 +275,9 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(PlanArgs a, DecodeAr
   if (tid == 0) pl.hdr->n_prefill = base;
   if (a.co_wgs > 0) {
     if (tid < 2) a.dec_rec[tid] = 0;
-    dec_rows = block_sum_1024(dec_rows, sum_lds);
-    dec_tiles = block_sum_1024(dec_tiles, sum_lds);
-    pairs = block_sum_1024(pairs, sum_lds);
-    if (tid == 0) pl.hdr->dec_wgs = pick_decode_wgs(a, dec_rows, dec_tiles, pairs);
+    float sums[3] = {dec_rows, dec_tiles, pairs};
+    block_sum3_1024(sums, sum_lds);
+    if (tid == 0) pl.hdr->dec_wgs = pick_decode_wgs(a, sums[0], sums[1], sums[2]);
   } else if (tid == 0) {
     pl.hdr->dec_wgs = 0;
   }
