@@ -93,7 +93,10 @@ def test_copy_and_fill_paths_match_oracle(device, kv, bs, monkeypatch):
     monkeypatch.setattr(lib, "nvs_attention_workspace_bytes_cache", lambda *a: plain(*a[:7]))
     fill_out, hdr = _run_checked(wl, ids, f"fill path {kv}/{bs}", holes)
     assert hdr[HDR_SHADOW_ON] == 0
-    # Decode rows come from the same kernel either way.
+    # Decode rows come from the same decode waves either way (inside the
+    # prefill launch with the copy, a decode launch of their own without it):
+    # with this few decode tiles (T <= 34) both split them over T / 4 groups
+    # alike.
     dec = [i for i, (p, n) in enumerate(spec) if n == 1]
     rows = np.concatenate([np.arange(int(wl.context.cu_seqlens_q[i]), int(wl.context.cu_seqlens_q[i + 1]))
                            for i in dec])
