@@ -115,6 +115,19 @@ def test_copy_over_capacity_falls_back_on_the_device(device):
     assert hdr[HDR_SHADOW_TILES] == 72 * 63 and hdr[HDR_SHADOW_ON] == 0
 
 
+def test_copy_over_capacity_with_decode_rows(device):
+    """The over-capacity batch with decode rows beside it: the prefill
+    launch's first work-groups still stream the decode rows (the plan turned
+    only its prefill part off), the classic kernel serves the prefill rows,
+    and the merge after them joins the split decode rows."""
+    say("code-cache prefill over capacity, decode rows")
+    spec = [(3998, 2)] * 72 + [(9000, 1), (4000, 1), (12000, 1)]
+    wl = _batch(spec, 32, 8, "fp8", seed=62)
+    ids = [0, 71, 72, 73, 74]
+    _, hdr = _run_checked(wl, ids, "copy over capacity, decode rows")
+    assert hdr[HDR_SHADOW_ON] == 0
+
+
 @pytest.mark.parametrize("g", [1, 2, 5, 8])
 def test_copy_path_gqa_groups(device, g):
     """Group sizes whose query tiling the two prefill kernels share (1, 2, 8:
