@@ -19,9 +19,15 @@ iteration, v_mfma_f32_32x32x16_bf16 (or _f16) throughout:
 Iteration j: segment A runs PV of tile j-1 beside the first exponentials of
 S_j (and, for a unit's first tile, its row max and the running max);
 segment B runs QK of tile j+1 beside the rest of S_j's exponentials, the
-bf16 packing of P_j and the row sums.  K/V operands are read from LDS into
-AGPR rings six operands ahead of their MFMAs; tiles are copied HBM -> LDS by
-buffer loads that write LDS directly (rows out of range read as zero).
+bf16 packing of P_j and the row sums, and, once its K operands are read,
+reads the first operands of tile j's PV.  K/V operands are read from LDS
+into AGPR rings six operands ahead of their MFMAs; tiles are copied HBM ->
+LDS by buffer loads that write LDS directly (rows out of range read as
+zero): K tile j+2 into K buffer j % 2 and V tile j+1 into V buffer
+(g+1) % 3, g counting the work-group's iterations (V tiles rotate through
+three buffers so the one segment B reads is complete a whole iteration
+before; the V address registers move to the current buffer once an
+iteration).
 
 From one unit into the next: the fills of unit u's last two iterations copy
 unit u+1's key tiles 0 and 1; u's last iteration reads u+1's query rows (in
@@ -48,7 +54,8 @@ Register map (fixed; the C++ side binds inputs to it):
   v[0:127]    S_j / S_{j+1}: S[par][kb][qb] = v[64 par + 16 (2 kb + qb) ..]
   v[128:191]  P_j / P_{j-1}: P[par][qb][m] = v[128 + 32 par + 16 qb + 4 m ..]
   v[192:199]  K operand LDS addresses, one per d-step st (K buffer 0, kb 0)
-  v[200:207]  V operand LDS addresses, per (d-block n, key half e)
+  v[200:207]  V operand LDS addresses, per (d-block n, key half e), in the
+              current V buffer (an in-out operand: the loop moves them)
   v[208:211]  fill lane offsets (K and V rows have one stride)
   v[212:215]  query-row copy lane offsets (row groups 0..3)
   v216-217 m_run, v218-219 l_run, v220-221 mask limit, v222 -inf,
@@ -62,7 +69,8 @@ Register map (fixed; the C++ side binds inputs to it):
   a[0:63]     Q^T operands: Q[qb][st] = a[32 qb + 4 st ..]
   a[64:191]   O^T accumulators: O[n][qb] = a[64 + 16 (2 n + qb) ..]
   a[192:223]  V operand ring (8 slots), a[224:255] K operand ring (8 slots)
-  s[4:23], s37, s60, s61 inputs, s[24:59] unit state, s[64:99] loop state
+  s[4:23], s37, s60, s61 inputs, s[24:59] unit state, s[64:99] loop state,
+  s100 the current iteration's V buffer (its offset from V buffer 0)
 """
 from __future__ import annotations
 
@@ -226,9 +234,17 @@ DT = ["s76", "s77", "s78", "s79", "s80", "s81", "s82", "s83", "s84", "s85", "s86
 S_U2IN = "s60"       # input: the work-group's third unit
 S_O4 = "s61"         # 4 output rows in bytes
 
-LDS_V0 = 32768      # V buffer 0 (K buffers at 0 and 16384)
+LDS_V0 = 32768      # V buffer 0 (K buffers at 0 and 16384; V buffers 1 and 2 follow)
 TILE = 16384        # bytes of one 64-key bf16 tile
+NVBUF = 3           # V buffers: the tile of iteration g in buffer g % 3
+S_VB = "s100"       # offset from V buffer 0 of the buffer of the current iteration's tile
+BANK_NV0 = (34, 35)  # the unit's value tile 0: lo, hi (its bytes are key tile 0's)
 RSRC_W3 = "0x20000"  # raw buffer: 32-bit data format, no swizzle, no stride
+
+
+PAIR_WAITS = True  # one lgkmcnt wait for each pair of K or V operands
+FILL_SLOTS = 24  # segment A slots the fills' set-up and loads are spread over
+V_FILL_FIRST = False  # the V fill's loads ahead of the K fill's tile rows
 
 
 class Emitter:
@@ -244,7 +260,13 @@ class Emitter:
         self.lds.append(tag)
 
     def lds_wait(self, tag):
-        """Wait until the LDS op `tag` has completed (LDS returns in order)."""
+        """Wait until the LDS op `tag` has completed (LDS returns in order).
+        With PAIR_WAITS, the wait for an even operand covers the odd one
+        after it when that was read too: one wait a pair of operands."""
+        if PAIR_WAITS and tag[0] in ("v", "k") and tag[1] % 2 == 0:
+            nxt = (tag[0], tag[1] + 1) + tag[2:]
+            if nxt in self.lds:
+                tag = nxt
         if tag not in self.lds:
             return
         i = self.lds.index(tag)
@@ -421,13 +443,36 @@ def spread(items, slots):
 
 
 # ------------------------------------------------------------ LDS reads
-def v_read(em, par_buf, i):
-    """V operand i (m = i // 4, n = i % 4) of the V buffer par_buf into ring slot i % 8."""
+def v_read(em, i):
+    """V operand i (m = i // 4, n = i % 4) into ring slot i % 8, from the V
+    buffer the VADDR registers point at (they move with the iterations)."""
     m, n = divmod(i, 4)
     _, lo, hi = VSLOT(i % 8)
-    off = TILE * par_buf + 4096 * m
+    off = 4096 * m
     em.lds_issue(("v", i, 0), f"ds_read_b64_tr_b16 {lo}, {VADDR[(n, 0)]} offset:{off}")
     em.lds_issue(("v", i, 1), f"ds_read_b64_tr_b16 {hi}, {VADDR[(n, 1)]} offset:{off}")
+
+
+def early_tags():
+    """The LDS reads outstanding when an iteration with a PV starts: the
+    first AHEAD V operands, read by the iteration before."""
+    return [("v", i, e) for i in range(AHEAD) for e in (0, 1)]
+
+
+def v_rotate_items():
+    """VADDR from the previous iteration's V buffer to the current one's
+    (S_VB): + TILE, or - 2 TILE from buffer 2 back to buffer 0.  The SCC
+    pair and its move stay together."""
+    return [[f"s_mov_b32 {S_TMP}, {TILE}", f"s_cmp_eq_u32 {S_VB}, 0",
+             f"s_cselect_b32 {S_TMP}, {-2 * TILE & 0xffffffff:#x}, {S_TMP}"]] + \
+        [f"v_add_u32 {VADDR[(n, e)]}, {S_TMP}, {VADDR[(n, e)]}" for n in range(4) for e in range(2)]
+
+
+def vb_advance(em):
+    """S_VB to the next iteration's V buffer."""
+    em(f"s_add_u32 {S_VB}, {S_VB}, {TILE}")
+    em(f"s_cmp_eq_u32 {S_VB}, {NVBUF * TILE}")
+    em(f"s_cselect_b32 {S_VB}, 0, {S_VB}")
 
 
 def k_read(em, par_buf, i):
@@ -450,17 +495,15 @@ def qk_mfmas(i, spar):
 
 
 AHEAD = 6  # operands read ahead of their MFMAs (at most 7: the rings hold 8)
-READ_EARLY = True  # issue each read-ahead right after the slot's first MFMA
-V_FIRST = True  # issue segment A's first V reads before the fills' set-up
 NA = 12  # exponential pairs of segment A
 
 
-def read_ahead_a(em, ppar, spar, i, last=False):
+def read_ahead_a(em, spar, i, last=False):
     """Segment A's read-ahead after PV operand i: V operand i + AHEAD, or,
     in the last AHEAD slots, the first K operands of segment B (none in a
     unit's last iteration, whose segment B has no QK^T)."""
     if i + AHEAD < 16:
-        v_read(em, ppar, i + AHEAD)
+        v_read(em, i + AHEAD)
     elif not last:
         k_read(em, spar, i + AHEAD - 16)
 
@@ -477,14 +520,17 @@ def mark(em, k):
 
 
 # ------------------------------------------------------------------ fills
-def fill_tile(paged, which, row, tile, blk, par_dst, nxt=None):
-    """Instructions that copy one 64-key tile (K or V) into buffer par_dst:
-    row = first cache row of the tile (SGPR), tile = SGPR holding its index
-    (for the row count), blk = its block id (paged; < 0: missing).  nxt =
-    "sel": tile index ntiles is the next unit's key tile 0 instead; "one":
-    the next unit's key tile 1.  Returns a list whose items are
-    instruction strings or groups (lists) that must stay together: each m0
-    write, its wait state and its direct-to-LDS load."""
+def fill_tile(paged, which, row, tile, blk, par_dst, nxt=None, tile_add=0):
+    """Instructions that copy one 64-key tile (K or V) into LDS: a K tile
+    into K buffer par_dst, a V tile into the V buffer after S_VB's (the
+    next iteration's).  row = first cache row of the tile (SGPR), tile =
+    SGPR holding its index less tile_add (for the row count), blk = its
+    block id (paged; < 0: missing).  nxt = "sel": tile index ntiles is the
+    next unit's key tile 0 instead; "one": the next unit's key tile 1;
+    "v0": the next unit's value tile 0 (read from its bank).  Returns a
+    list whose items are instruction strings or groups (lists) that must
+    stay together: each m0 write, its wait state and its direct-to-LDS
+    load, and each lane read with the wait states before its loads."""
     base_lo, base_hi = (S_KBASE_LO, S_KBASE_HI) if which == "k" else (S_VBASE_LO, S_VBASE_HI)
     rowb = S_KROW if which == "k" else S_VROW
     rs = S_RK_W if which == "k" else S_RV_W
@@ -498,6 +544,10 @@ def fill_tile(paged, which, row, tile, blk, par_dst, nxt=None):
         f"s_addc_u32 {rs[1]}, {rs[1]}, {base_hi}",
         # rows of the tile that hold keys: clamp(K - 64 t, 0, 64)
         f"s_lshl_b32 {t0}, {tile}, 6",
+    ]
+    if tile_add:
+        out.append(f"s_add_u32 {t0}, {t0}, {64 * tile_add}")
+    out += [
         f"s_sub_i32 {t0}, {S_K}, {t0}",
         f"s_max_i32 {t0}, {t0}, 0",
         f"s_min_i32 {t0}, {t0}, 64",
@@ -514,12 +564,23 @@ def fill_tile(paged, which, row, tile, blk, par_dst, nxt=None):
     elif nxt == "one":  # the next unit's tile 1, whatever this unit's are
         out = [f"s_mov_b32 {rs[0]}, {S_NK[1][0]}", f"s_mov_b32 {rs[1]}, {S_NK[1][1]}",
                f"s_mov_b32 {rs[2]}, {S_NREC[1]}"]
+    elif nxt == "v0":  # the next unit's value tile 0 (as many rows as its key tile 0)
+        out = [[f"v_readlane_b32 {rs[0]}, {BANKN}, {BANK_NV0[0]}",
+                f"v_readlane_b32 {rs[1]}, {BANKN}, {BANK_NV0[1]}", "s_nop 4"],
+               f"s_mov_b32 {rs[2]}, {S_NREC[0]}"]
     out.append(f"s_and_b32 {rs[1]}, {rs[1]}, 0xffff")
     out.append(f"s_mov_b32 {rs[3]}, {RSRC_W3}")
-    dst = (0 if which == "k" else LDS_V0) + TILE * par_dst
-    for i in range(4):
-        out.append([f"s_add_u32 m0, {S_M0W}, {dst + 1024 * i}", "s_nop 0",
-                    f"buffer_load_dwordx4 {offs[i]}, {rsrc}, 0 offen lds"])
+    if which == "k":
+        for i in range(4):
+            out.append([f"s_add_u32 m0, {S_M0W}, {TILE * par_dst + 1024 * i}", "s_nop 0",
+                        f"buffer_load_dwordx4 {offs[i]}, {rsrc}, 0 offen lds"])
+    else:
+        vb = S_T[3]  # the V buffer after S_VB's, + the wave's rows
+        out += [[f"s_add_u32 {vb}, {S_VB}, {TILE}", f"s_cmp_eq_u32 {vb}, {NVBUF * TILE}",
+                 f"s_cselect_b32 {vb}, 0, {vb}"], f"s_add_u32 {vb}, {vb}, {S_M0W}"]
+        for i in range(4):
+            out.append([f"s_add_u32 m0, {vb}, {LDS_V0 + 1024 * i}", "s_nop 0",
+                        f"buffer_load_dwordx4 {offs[i]}, {rsrc}, 0 offen lds"])
     return out
 
 
@@ -548,26 +609,33 @@ def advance_tile(em):
     em(f"s_add_u32 {S_LB}, {S_LB}, {S_T[3]}")
 
 
-def issue_block_id(em):
-    """Vector load of the block id of logical block S_LB into BLKV (every
-    lane the same address); S_BOK records whether S_LB is a block of the
-    sequence.  The loop's vmcnt(0) before each barrier completes it."""
-    em(f"s_lshl_b32 {S_T[2]}, {S_LB}, 2")
-    em(f"v_mov_b32 {ET[0]}, {S_T[2]}")
-    em(f"buffer_load_dword {BLKV}, {ET[0]}, {S_RBT}, 0 offen")
-    em(f"s_cmp_lt_u32 {S_T[2]}, {S_RBT_NREC}")
-    em(f"s_cselect_b32 {S_BOK}, 1, 0")
-
-
-def take_block_id(em, dst):
-    """dst <- the block id loaded by issue_block_id, or -1 where the
-    logical block is past the sequence's or the id is outside the pool."""
-    em(f"v_readfirstlane_b32 {dst}, {BLKV}")
-    em("s_nop 0")
-    em(f"s_cmp_lt_u32 {dst}, {S_NB}")
-    em(f"s_cselect_b32 {dst}, {dst}, -1")
-    em(f"s_cmp_eq_u32 {S_BOK}, 0")
-    em(f"s_cselect_b32 {dst}, -1, {dst}")
+def tile_rows_items(paged, first):
+    """The fills' tile j+2, as items for the slots of segment A: its block id
+    (paged: from the record for a first tile, else taken from the load of
+    the iteration before) and cache row, S_KOFF and S_LB moved on, and the
+    load of tile j+3's block id issued (in place in BLKV); then S_T[2] =
+    j + 2.  Each SCC pair, and the lane read with its wait state, is a
+    group."""
+    it = []
+    if paged:
+        d = S_B[2]
+        if first:
+            it.append(f"s_mov_b32 {d}, {S_BLK012[2]}")
+        else:
+            it.append([f"v_readfirstlane_b32 {d}, {BLKV}", "s_nop 0", f"s_cmp_lt_u32 {d}, {S_NB}",
+                       f"s_cselect_b32 {d}, {d}, -1"])
+            it.append([f"s_cmp_eq_u32 {S_BOK}, 0", f"s_cselect_b32 {d}, -1, {d}"])
+        it += [f"s_max_i32 {S_T[2]}, {d}, 0", f"s_mul_i32 {S_ROW[2]}, {S_T[2]}, {S_BS}",
+               f"s_add_u32 {S_ROW[2]}, {S_ROW[2]}, {S_KOFF}"]
+        it.append([f"s_add_u32 {S_KOFF}, {S_KOFF}, 64", f"s_cmp_eq_u32 {S_KOFF}, {S_BS}",
+                   f"s_cselect_b32 {S_KOFF}, 0, {S_KOFF}", f"s_cselect_b32 {S_T[3]}, 1, 0"])
+        it += [f"s_add_u32 {S_LB}, {S_LB}, {S_T[3]}", f"s_lshl_b32 {S_T[2]}, {S_LB}, 2",
+               f"v_mov_b32 {BLKV}, {S_T[2]}", f"buffer_load_dword {BLKV}, {BLKV}, {S_RBT}, 0 offen"]
+        it.append([f"s_cmp_lt_u32 {S_T[2]}, {S_RBT_NREC}", f"s_cselect_b32 {S_BOK}, 1, 0"])
+    else:
+        it += [f"s_add_u32 {S_T[2]}, {S_J}, 2", f"s_lshl_b32 {S_ROW[2]}, {S_T[2]}, 6"]
+    it.append(f"s_add_u32 {S_T[2]}, {S_J}, 2")
+    return it
 
 
 # ----------------------------------------------------------------- blocks
@@ -710,10 +778,11 @@ def decode(em, u, paged, bank=None):
         em(f"s_addc_u32 {c1}, {c1}, {m1}")
         em(f"v_writelane_b32 {BANKN}, {c0}, {lanes[0]}")
         em(f"v_writelane_b32 {BANKN}, {c1}, {lanes[1]}")
-        if base == BANKC_KC:
-            kb_lo, kb_hi = t[20], t[21]
-            em(f"s_mov_b32 {kb_lo}, {c0}")
-            em(f"s_mov_b32 {kb_hi}, {c1}")
+        kb_lo, kb_hi = (t[20], t[21]) if base == BANKC_KC else (t[22], t[23])
+        em(f"s_mov_b32 {kb_lo}, {c0}")
+        em(f"s_mov_b32 {kb_hi}, {c1}")
+    vb_lo, vb_hi = t[22], t[23]
+    kb_lo, kb_hi = t[20], t[21]
     # key tiles 0 and 1 of the unit (what a fill of tile t reads)
     for tl in range(2):
         lo, hi, rec = c0, c1, c2
@@ -745,6 +814,13 @@ def decode(em, u, paged, bank=None):
         em(f"v_writelane_b32 {BANKN}, {lo}, {BANK_NK[tl][0]}")
         em(f"v_writelane_b32 {BANKN}, {hi}, {BANK_NK[tl][1]}")
         em(f"v_writelane_b32 {BANKN}, {rec}, {BANK_NK[tl][2]}")
+        if tl == 0:  # the value tile 0: the same rows of the value base
+            em(f"s_mul_i32 {lo}, {m0}, {S_KROW}")
+            em(f"s_mul_hi_u32 {hi}, {m0}, {S_KROW}")
+            em(f"s_add_u32 {lo}, {lo}, {vb_lo}")
+            em(f"s_addc_u32 {hi}, {hi}, {vb_hi}")
+            em(f"v_writelane_b32 {BANKN}, {lo}, {BANK_NV0[0]}")
+            em(f"v_writelane_b32 {BANKN}, {hi}, {BANK_NV0[1]}")
     # block-table row: bt + b x row bytes
     readlanes(em, [(c0, BANKC, BANKC_BT[0]), (c1, BANKC, BANKC_BT[1]), (c2, BANKC, BANKC_BTS)])
     em(f"s_mul_i32 {m0}, {b}, {c2}")
@@ -865,10 +941,11 @@ def q_prefetch(em, bank, guard=False):
             em(f"buffer_load_dwordx4 {QLANE[i % 4]}, {rs}, {0 if i < 4 else S_Q16} offen lds")
 
 
-def k_prefetch(em, tiles):
-    """Key tiles 0 and 1 of a unit into K buffers 0 and 1 (rows 16 w ..
-    16 w + 15 of each, as the loop's fills): tiles = ((lo, hi, bytes), ...)
-    SGPR names."""
+def k_prefetch(em, tiles, bank):
+    """Key tiles 0 and 1 of a unit into K buffers 0 and 1 and its value tile
+    0 into V buffer S_VB (the next iteration's), rows 16 w .. 16 w + 15 of
+    each, as the loop's fills: tiles = ((lo, hi, bytes), ...) SGPR names,
+    bank = the unit's bank (the value tile's address)."""
     for t, ((lo, hi, rec), rs_w) in enumerate(zip(tiles, (S_RK_W, S_RV_W))):
         em(f"s_mov_b32 {rs_w[0]}, {lo}")
         em(f"s_and_b32 {rs_w[1]}, {hi}, 0xffff")
@@ -879,6 +956,17 @@ def k_prefetch(em, tiles):
             em(f"s_add_u32 m0, {S_M0W}, {TILE * t + 1024 * i}")
             em("s_nop 0")
             em(f"buffer_load_dwordx4 {DMAK[i]}, {rsrc}, 0 offen lds")
+    # the value tile: as many rows as key tile 0
+    em(f"v_readlane_b32 {S_RK_W[0]}, {bank}, {BANK_NV0[0]}")
+    em(f"v_readlane_b32 {S_RK_W[1]}, {bank}, {BANK_NV0[1]}")
+    em("s_nop 4")
+    em(f"s_and_b32 {S_RK_W[1]}, {S_RK_W[1]}, 0xffff")
+    em(f"s_mov_b32 {S_RK_W[2]}, {tiles[0][2]}")
+    em(f"s_add_u32 {S_TMP}, {S_VB}, {S_M0W}")
+    for i in range(4):
+        em(f"s_add_u32 m0, {S_TMP}, {LDS_V0 + 1024 * i}")
+        em("s_nop 0")
+        em(f"buffer_load_dwordx4 {DMAK[i]}, {S_RK}, 0 offen lds")
 
 
 def q_read_step(em, st, tmp):
@@ -1056,37 +1144,36 @@ def block_iteration(em, paged, par, kind, lbl):
       last    a unit's last tile ending the pipeline: no K fill, no QK^T,
       lastc   a unit's last tile chaining into the next: the next unit's
               Q^T read and QK^T of its tile 0.
-    Fills: K tile j+2 (or the next unit's tile 0 / 1) and V tile j, spread
-    over segment A.  Paged: the block id of tile j+2 (from the record for a
-    first tile, else loaded an iteration earlier) is taken and the load of
-    tile j+3's issued.  Iterations after the first read the claim slot and
-    load the claimed unit's plan record."""
+    Fills: K tile j+2 (or the next unit's tile 0 / 1) and V tile j+1 (or
+    the next unit's tile 0; none in a last iteration), spread over segment
+    A.  Paged: the block id of tile j+2 (from the record for a first tile,
+    else loaded an iteration earlier) is taken and the load of tile j+3's
+    issued.  Iterations after the first read the claim slot and load the
+    claimed unit's plan record.  V operand reads: segment A's PV reads
+    operands AHEAD.. (the iteration before read the first AHEAD), the VADDR
+    registers then move to this iteration's V buffer and segment B reads
+    the first AHEAD operands of the PV of tile j, behind its QK^T's K
+    operand reads."""
     first = kind in ("fresh0", "chain0")
     pv = kind != "fresh0"
     qk = kind != "last"
     ppar, spar = 1 - par, 1 - par
+    em.lds = early_tags() if pv else []
     if kind == "lastc":  # the next unit's query rows, copied at the unit's start
         em("s_waitcnt vmcnt(0)")
-    if pv and V_FIRST:
-        for i in range(AHEAD):
-            v_read(em, ppar, i)
-    # ---- tile rows of the fills
-    if paged:
-        if first:
-            em(f"s_mov_b32 {S_B[2]}, {S_BLK012[2]}")
-        else:
-            take_block_id(em, S_B[2])
-        block_row(em, S_ROW[2], S_B[2])
-        advance_tile(em)
-        issue_block_id(em)  # tile j+3, taken at iteration j+1
-    else:
-        em(f"s_add_u32 {S_T[2]}, {S_J}, 2")
-        em(f"s_lshl_b32 {S_ROW[2]}, {S_T[2]}, 6")
-    em(f"s_add_u32 {S_T[2]}, {S_J}, 2")
     mark(em, 0)
-    fill = [] if kind == "last" else fill_tile(paged, "k", S_ROW[2], S_T[2], S_B[2] if paged else None, par,
+    if kind == "lastc":
+        vfill = fill_tile(paged, "v", None, None, None, None, nxt="v0")
+    elif kind != "last":
+        vfill = fill_tile(paged, "v", S_ROW[1], S_J, S_B[1] if paged else None, None, tile_add=1)
+    else:
+        vfill = []
+    fill = vfill if V_FILL_FIRST else []
+    fill += tile_rows_items(paged, first)
+    fill += [] if kind == "last" else fill_tile(paged, "k", S_ROW[2], S_T[2], S_B[2] if paged else None, par,
                                                nxt="one" if kind == "lastc" else "sel")
-    fill += fill_tile(paged, "v", S_ROW[0], S_J, S_B[0] if paged else None, par)
+    if not V_FILL_FIRST:
+        fill += vfill
     # ---- segment A
     pairs = exp_pairs(par)
     touched = set()
@@ -1105,23 +1192,28 @@ def block_iteration(em, paged, par, kind, lbl):
     if not pv:
         emit_items(em, fill)
         emit_items(em, a_items)
+        emit_items(em, v_rotate_items())
         mark(em, 1)
         for i in range(AHEAD):
             k_read(em, spar, i)
     else:
         lead = 0  # VALU work before the first MFMA (none: measured fastest of 0, 2, 4, 6, 8, 12)
         emit_items(em, a_items[:lead])
-        # the fill's scalar setup and loads share the first 24 slots (of 8,
-        # 16, 24 or 32: measured fastest)
+        # the fill's scalar setup and loads share the first FILL_SLOTS slots
         slots = spread(a_items[lead:], 32)
-        fs = spread(fill, 24)
-        for k in range(24):
+        fs = spread(fill, FILL_SLOTS)
+        for k in range(FILL_SLOTS):
             slots[k] = fs[k] + slots[k]
+        # the VADDR move after the last V read (at step 15 - AHEAD)
+        rot = v_rotate_items()
+        slots[24] = [rot[0]] + slots[24]
+        for k, x in enumerate(rot[1:]):
+            slots[25 + k % 7] = [x] + slots[25 + k % 7]
         for i in range(16):
             em.lds_wait(("v", i, 1))
             mf = pv_mfmas(em, i, ppar)
             em(mf[0])
-            read_ahead_a(em, ppar, spar, i, not qk)
+            read_ahead_a(em, spar, i, not qk)
             if kind == "lastc" and 1 <= i <= 8:
                 q_read_step(em, i - 1, AL[0])
             emit_items(em, slots[2 * i])
@@ -1136,10 +1228,14 @@ def block_iteration(em, paged, par, kind, lbl):
         em(mf[0])
         if i + AHEAD < 16:
             k_read(em, spar, i + AHEAD)
+        else:  # the next PV's first operands, from this iteration's V buffer
+            v_read(em, i + AHEAD - 16)
         emit_items(em, slots[2 * i])
         em(mf[1])
         emit_items(em, slots[2 * i + 1])
     if not qk:
+        for i in range(AHEAD):
+            v_read(em, i)
         emit_items(em, b_items)
     # The tile's row sums, taken with the running max of the tiles before:
     # past SUM_LIMIT or not finite (a max that was stale or still -inf) on
@@ -1160,6 +1256,7 @@ def block_iteration(em, paged, par, kind, lbl):
         em(f"s_mov_b32 {S_B[1]}, {S_B[2]}")
     em(f"s_mov_b32 {S_ROW[0]}, {S_ROW[1]}")
     em(f"s_mov_b32 {S_ROW[1]}, {S_ROW[2]}")
+    vb_advance(em)
     # chain0's output stores and the next unit's query-row copies (its last
     # 32 vector memory operations) may drain
     em(f"s_waitcnt vmcnt({32 if kind == 'chain0' else 0})")
@@ -1168,7 +1265,6 @@ def block_iteration(em, paged, par, kind, lbl):
         claim_publish(em, lbl)
     em("s_barrier")
     mark(em, 4)
-    em.lds = []
 
 
 def block_slow(em, par, lbl):
@@ -1247,15 +1343,14 @@ def block_prologue(em):
 
 
 def block_pv_only(em, par):
-    """PV of the last tile (V and P of parity par)."""
-    for i in range(AHEAD):
-        v_read(em, par, i)
+    """PV of the last tile (P of parity par): its first AHEAD V operands
+    were read by the last iteration."""
     for i in range(16):
         em.lds_wait(("v", i, 1))
         for x in pv_mfmas(em, i, par):
             em(x)
         if i + AHEAD < 16:
-            v_read(em, par, i + AHEAD)
+            v_read(em, i + AHEAD)
     em.lds_drain()
 
 
@@ -1278,6 +1373,7 @@ def program(paged):
     em("s_nop 4")
     em(f"v_mov_b32 {NINF}, 0xff800000")
     em(f"s_mov_b32 {S_IT}, 0")
+    em(f"s_mov_b32 {S_VB}, 0")
     # ---- the work-group's first three units (claimed by the caller): the
     # first two decoded, the third's record loaded by the first's start
     emit_items(em, record_load_items(S_U0))
@@ -1298,7 +1394,7 @@ def program(paged):
         regs = DT[12 + 3 * tl: 15 + 3 * tl]  # not the fill resources k_prefetch writes
         cur.append(tuple(regs))
         readlanes(em, [(regs[0], BANKU, lo), (regs[1], BANKU, hi), (regs[2], BANKU, rec)])
-    k_prefetch(em, cur)
+    k_prefetch(em, cur, BANKU)
     em(f"{u}s0:")
     em("s_waitcnt vmcnt(0)")
     em("s_barrier")
@@ -1373,7 +1469,7 @@ def program(paged):
         em.lds = []
         em(f"s_cmp_eq_u32 {S_NNT}, 0")
         em(f"s_cbranch_scc1 {u}d{par}nonext")
-        k_prefetch(em, [(lo, hi, rec) for (lo, hi), rec in zip(S_NK, S_NREC)])
+        k_prefetch(em, [(lo, hi, rec) for (lo, hi), rec in zip(S_NK, S_NREC)], BANKN)
         q_read(em)
         em(f"{u}d{par}nonext:")
         block_pv_only(em, par)
@@ -1399,7 +1495,7 @@ def program(paged):
     em("s_barrier")
     em(f"s_cmp_eq_u32 {S_NNT}, 0")
     em(f"s_cbranch_scc1 {u}znonext")
-    k_prefetch(em, [(lo, hi, rec) for (lo, hi), rec in zip(S_NK, S_NREC)])
+    k_prefetch(em, [(lo, hi, rec) for (lo, hi), rec in zip(S_NK, S_NREC)], BANKN)
     q_read(em)
     em(f"{u}znonext:")
     zero_output(em, BANKU)
@@ -1433,7 +1529,7 @@ CLOBBERS = (
     [f"v{i}" for i in range(0, 192)] + [f"v{i}" for i in range(216, 246)] + [f"v{i}" for i in range(249, 253)]
     + [f"a{i}" for i in range(0, 256)]
     + [f"s{i}" for i in range(24, 32)] + [f"s{i}" for i in range(34, 37)] + ["s38", "s39"]
-    + [f"s{i}" for i in range(40, 54)] + [f"s{i}" for i in range(56, 60)] + [f"s{i}" for i in range(64, 100)]
+    + [f"s{i}" for i in range(40, 54)] + [f"s{i}" for i in range(56, 60)] + [f"s{i}" for i in range(64, 101)]
     + ["vcc", "scc", "m0", "memory"]
 )
 
