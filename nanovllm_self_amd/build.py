@@ -60,9 +60,11 @@ def _compile(src: Path) -> Path:
 
 
 def generate() -> None:
-    """Regenerate the prefill kernel's tile loop (csrc/prefill_mx_asm.inc) and
-    check that every register it writes is declared to the compiler."""
-    for script in ("gen_prefill_mx.py", "check_prefill_mx.py"):
+    """Regenerate the prefill kernel's tile loop (csrc/prefill_mx_asm.inc),
+    check that every register it writes is declared to the compiler, and run
+    the loop on the CPU over a few random batches for its LDS waits and
+    barriers and the tiles its MFMAs read."""
+    for script in ("gen_prefill_mx.py", "check_prefill_mx.py", "check_prefill_lds.py"):
         res = subprocess.run([sys.executable, str(CSRC / script)], capture_output=True, text=True)
         if res.returncode != 0:
             raise RuntimeError(f"{script} failed:\n{res.stdout}{res.stderr}")
