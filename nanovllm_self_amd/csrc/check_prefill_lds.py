@@ -17,7 +17,9 @@ one trace stands for all four, with:
     MFMAs) and the V operands of each PV tile come from one fill of one
     buffer, and the tiles read, in order, are each claimed unit's tiles in
     order (the plan records are modelled on schedule.hip's plan kernel).
-The arithmetic of scores and outputs is not interpreted.  Run by the build
+Every buffer load and store is checked to use a raw resource (word 3) with
+no stride and a 48-bit base.  The arithmetic of scores and outputs is not
+interpreted.  Run by the build
 with a few batches; `python check_prefill_lds.py SEED BATCHES` runs more."""
 import importlib.util
 import os
@@ -386,8 +388,7 @@ class Sim:
             self.lds_write(addr)
         elif op == "buffer_load_dword":
             rs = args[2]
-            m = re.fullmatch(r"s\[(\d+):(\d+)\]", rs)
-            r0 = int(m.group(1))
+            r0 = self.check_rsrc(rs)
             base = self.s[r0] | ((self.s[r0 + 1] & 0xFFFF) << 32)
             nrec = self.s[r0 + 2]
             voff = self.vget(args[1])
@@ -403,13 +404,13 @@ class Sim:
             else:
                 raise NotImplementedError(ln)
         elif op == "buffer_load_dwordx4":
-            m = re.fullmatch(r"s\[(\d+):(\d+)\]", args[1])
-            r0 = int(m.group(1))
+            r0 = self.check_rsrc(args[1])
             base = self.s[r0] | ((self.s[r0 + 1] & 0xFFFF) << 32)
             nrec = self.s[r0 + 2]
             assert args[-1].endswith("lds"), ln
             self.lds_fill(self.m0, (base, nrec) if nrec else ("zero",))
         elif op == "buffer_store_dwordx4":
+            self.check_rsrc(args[2])
             self.vmq.append({"pos": self.pos, "done": None, "region": None})
         elif op == "global_atomic_add":
             self.vmq.append({"pos": self.pos, "done": None, "region": None})
@@ -418,6 +419,16 @@ class Sim:
             self.counter += 1
         else:
             raise NotImplementedError(op)
+
+    def check_rsrc(self, tok):
+        """A buffer resource as the loop must build it: raw (word 3), no
+        stride and a 48-bit base (word 1's high half zero)."""
+        m = re.fullmatch(r"s\[(\d+):(\d+)\]", tok)
+        r0 = int(m.group(1))
+        w1, w3 = self.s.get(r0 + 1, 0xDEADBEEF), self.s.get(r0 + 3, 0xDEADBEEF)
+        if w3 != int(G.RSRC_W3, 16) or w1 >> 16:
+            self.fail(f"buffer resource {tok}: word 1 {w1:#x}, word 3 {w3:#x}")
+        return r0
 
     @staticmethod
     def off(args):

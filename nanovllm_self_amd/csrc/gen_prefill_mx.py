@@ -530,7 +530,8 @@ def fill_tile(paged, which, row, tile, blk, par_dst, nxt=None, tile_add=0):
     "v0": the next unit's value tile 0 (read from its bank).  Returns a
     list whose items are instruction strings or groups (lists) that must
     stay together: each m0 write, its wait state and its direct-to-LDS
-    load, and each lane read with the wait states before its loads."""
+    load, each SCC write with its readers, and each lane read with the wait
+    states before its loads."""
     base_lo, base_hi = (S_KBASE_LO, S_KBASE_HI) if which == "k" else (S_VBASE_LO, S_VBASE_HI)
     rowb = S_KROW if which == "k" else S_VROW
     rs = S_RK_W if which == "k" else S_RV_W
@@ -554,13 +555,13 @@ def fill_tile(paged, which, row, tile, blk, par_dst, nxt=None, tile_add=0):
         f"s_mul_i32 {rs[2]}, {t0}, {rowb}",
     ]
     if paged:
-        out += [f"s_cmp_lt_i32 {blk}, 0", f"s_cselect_b32 {rs[2]}, 0, {rs[2]}"]
+        out.append([f"s_cmp_lt_i32 {blk}, 0", f"s_cselect_b32 {rs[2]}, 0, {rs[2]}"])
     if nxt == "sel":  # tile index = ntiles: the next unit's tile 0
-        out += [
+        out.append([
             f"s_cmp_eq_u32 {tile}, {S_NT}",
             f"s_cselect_b64 s[{rs[0][1:]}:{rs[1][1:]}], s[{S_NK[0][0][1:]}:{S_NK[0][1][1:]}], s[{rs[0][1:]}:{rs[1][1:]}]",
             f"s_cselect_b32 {rs[2]}, {S_NREC[0]}, {rs[2]}",
-        ]
+        ])
     elif nxt == "one":  # the next unit's tile 1, whatever this unit's are
         out = [f"s_mov_b32 {rs[0]}, {S_NK[1][0]}", f"s_mov_b32 {rs[1]}, {S_NK[1][1]}",
                f"s_mov_b32 {rs[2]}, {S_NREC[1]}"]
